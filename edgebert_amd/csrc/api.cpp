@@ -1,0 +1,792 @@
+// api.cpp -- host side of the C ABI: weight store, workspace, forward.
+//
+// Mirrors the reference's Model (src/lib.rs:40-106, 155-260, 573-666):
+//   ebh_create / ebh_set_tensor / ebh_finalize   <- Model::from_weights
+//   ebh_forward                                  <- Model::forward
+//   ebh_encode / ebh_encode_device               <- encode_uncached (after tokenisation)
+// All device work of one model runs on one HIP stream in this order:
+//   pack -> embed+LN -> L x [QKV GEMM, attention, out GEMM(+res), LN,
+//   up GEMM(+GELU), down GEMM(+res), LN] -> pool(+normalise).
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <mutex>
+#include <string>
+#include <unordered_map>
+#include <vector>
+
+#include "../../include/edgebert_hip.h"
+#include "../../include/edgebert_hip_ops.h"
+#include "internal.hpp"
+#include "kernels.hpp"
+
+namespace {
+thread_local std::string g_err;
+}  // namespace
+
+namespace ebh {
+int set_error(int code, const char* fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    g_err = buf;
+    return code;
+}
+}  // namespace ebh
+
+namespace {
+
+using ebh::set_error;
+#define fail set_error
+
+#define HIP_TRY(expr)                                                                     \
+    do {                                                                                  \
+        hipError_t e_ = (expr);                                                           \
+        if (e_ != hipSuccess)                                                             \
+            return fail(EBH_ERR_HIP, "%s failed: %s", #expr, hipGetErrorString(e_));      \
+    } while (0)
+
+constexpr size_t kAlign = 256;
+size_t align_up(size_t x) { return (x + kAlign - 1) / kAlign * kAlign; }
+
+struct HostTensor {
+    std::vector<float> data;
+    std::vector<int64_t> shape;
+};
+
+struct DevLayer {
+    float *wqkv, *bqkv, *wo, *bo, *ln1_g, *ln1_b, *w1, *b1, *w2, *b2, *ln2_g, *ln2_b;
+    uint16_t *wqkv16, *wo16, *w116, *w216;
+};
+
+struct Workspace {
+    void* base = nullptr;
+    int64_t tok_cap = 0;  // B*S tokens
+    int b_cap = 0;
+    float *X, *Y, *QKV, *CTX, *F;
+    int *ids, *mask, *counts, *cu, *ntok, *tok_id, *tok_pos, *err;
+    float* out;
+};
+
+struct ProfPair {
+    hipEvent_t a, b;
+};
+
+}  // namespace
+
+struct ebh_model {
+    ebh_config cfg{};
+    int dtype = EBH_DTYPE_F32;
+    int device = -1;
+    bool finalized = false;
+    std::unordered_map<std::string, HostTensor> host;
+    // device weights: one allocation
+    void* wbase = nullptr;
+    float *word, *pos, *type0, *emb_g, *emb_b;
+    std::vector<DevLayer> layers;
+    hipStream_t stream = nullptr;
+    hipEvent_t done = nullptr;  // completion of the last enqueued forward
+    bool has_done = false;
+    Workspace ws;
+    int last_B = 0;
+    // pinned host staging for the blocking API
+    int* h_ids = nullptr;
+    int* h_mask = nullptr;
+    float* h_out = nullptr;
+    int* h_err = nullptr;
+    int64_t h_cap = 0, h_out_cap = 0;
+    // profiling of one kernel family
+    int prof_kind = EBH_PROF_NONE;
+    std::vector<ProfPair> prof_events;
+    std::vector<hipEvent_t> prof_free;
+    std::mutex mu;
+};
+
+namespace {
+
+// Expected HF tensor names and shapes (src/lib.rs:161-238).
+std::vector<std::pair<std::string, std::vector<int64_t>>> expected_tensors(const ebh_config& c) {
+    const int64_t H = c.hidden_size, I = c.intermediate_size;
+    std::vector<std::pair<std::string, std::vector<int64_t>>> t = {
+        {"embeddings.word_embeddings.weight", {c.vocab_size, H}},
+        {"embeddings.position_embeddings.weight", {c.max_position_embeddings, H}},
+        {"embeddings.token_type_embeddings.weight", {c.type_vocab_size, H}},
+        {"embeddings.LayerNorm.weight", {H}},
+        {"embeddings.LayerNorm.bias", {H}},
+    };
+    for (int i = 0; i < c.num_hidden_layers; ++i) {
+        const std::string p = "encoder.layer." + std::to_string(i) + ".";
+        for (const char* proj : {"query", "key", "value"}) {
+            t.push_back({p + "attention.self." + proj + ".weight", {H, H}});
+            t.push_back({p + "attention.self." + proj + ".bias", {H}});
+        }
+        t.push_back({p + "attention.output.dense.weight", {H, H}});
+        t.push_back({p + "attention.output.dense.bias", {H}});
+        t.push_back({p + "attention.output.LayerNorm.weight", {H}});
+        t.push_back({p + "attention.output.LayerNorm.bias", {H}});
+        t.push_back({p + "intermediate.dense.weight", {I, H}});
+        t.push_back({p + "intermediate.dense.bias", {I}});
+        t.push_back({p + "output.dense.weight", {H, I}});
+        t.push_back({p + "output.dense.bias", {H}});
+        t.push_back({p + "output.LayerNorm.weight", {H}});
+        t.push_back({p + "output.LayerNorm.bias", {H}});
+    }
+    return t;
+}
+
+const std::vector<int64_t>* expected_shape(const ebh_config& c, const std::string& name,
+                                           std::vector<int64_t>& storage) {
+    for (auto& kv : expected_tensors(c))
+        if (kv.first == name) {
+            storage = kv.second;
+            return &storage;
+        }
+    return nullptr;
+}
+
+std::string shape_str(const int64_t* s, int n) {
+    std::string r = "[";
+    for (int i = 0; i < n; ++i) r += (i ? ", " : "") + std::to_string(s[i]);
+    return r + "]";
+}
+
+int check_config(const ebh_config& c) {
+    if (c.hidden_size <= 0 || c.num_attention_heads <= 0 || c.num_hidden_layers < 0 ||
+        c.intermediate_size <= 0 || c.vocab_size <= 0 || c.max_position_embeddings <= 0 ||
+        c.type_vocab_size <= 0 || !(c.layer_norm_eps >= 0.0f))
+        return fail(EBH_ERR_INVALID_ARG, "invalid config: sizes must be positive");
+    if (c.hidden_size % c.num_attention_heads)
+        return fail(EBH_ERR_INVALID_ARG, "hidden_size %d is not a multiple of num_attention_heads %d",
+                    c.hidden_size, c.num_attention_heads);
+    const int hd = c.hidden_size / c.num_attention_heads;
+    if (hd != 32 && hd != 64)
+        return fail(EBH_ERR_INVALID_ARG, "head_dim %d unsupported (32 or 64)", hd);
+    if (c.hidden_size % 8 || c.intermediate_size % 8)
+        return fail(EBH_ERR_INVALID_ARG, "hidden_size and intermediate_size must be multiples of 8");
+    if (c.hidden_size > 2048)
+        return fail(EBH_ERR_INVALID_ARG, "hidden_size %d above the supported 2048", c.hidden_size);
+    return EBH_OK;
+}
+
+void prof_begin(ebh_model* m, int kind, hipStream_t s, ProfPair& pp, bool& on) {
+    on = (m->prof_kind == kind);
+    if (!on) return;
+    for (hipEvent_t* e : {&pp.a, &pp.b}) {
+        if (!m->prof_free.empty()) {
+            *e = m->prof_free.back();
+            m->prof_free.pop_back();
+        } else {
+            (void)hipEventCreate(e);
+        }
+    }
+    (void)hipEventRecord(pp.a, s);
+}
+
+void prof_end(ebh_model* m, hipStream_t s, ProfPair& pp, bool on) {
+    if (!on) return;
+    (void)hipEventRecord(pp.b, s);
+    m->prof_events.push_back(pp);
+}
+
+int ensure_workspace(ebh_model* m, int B, int S) {
+    const int64_t T = (int64_t)B * S;
+    Workspace& w = m->ws;
+    if (w.base && T <= w.tok_cap && B <= w.b_cap) return EBH_OK;
+    const int64_t tcap = std::max<int64_t>(T, w.tok_cap);
+    const int bcap = std::max(B, w.b_cap);
+    const ebh_config& c = m->cfg;
+    const size_t H = c.hidden_size, I = c.intermediate_size;
+    size_t off = 0;
+    auto take = [&](size_t bytes) { size_t o = off; off += align_up(std::max<size_t>(bytes, 1)); return o; };
+    const size_t oX = take(tcap * H * 4), oY = take(tcap * H * 4), oQKV = take(tcap * 3 * H * 4),
+                 oCTX = take(tcap * H * 4), oF = take(tcap * I * 4), oIds = take(tcap * 4),
+                 oMask = take(tcap * 4), oCounts = take(bcap * 4), oCu = take((bcap + 1) * 4),
+                 oNtok = take(4), oTid = take(tcap * 4), oTpos = take(tcap * 4), oErr = take(4),
+                 oOut = take((size_t)bcap * H * 4);
+    // Work from the previous call may still use the old block.
+    if (m->has_done) HIP_TRY(hipEventSynchronize(m->done));
+    if (w.base) HIP_TRY(hipFree(w.base));
+    w.base = nullptr;
+    w.tok_cap = 0;
+    w.b_cap = 0;
+    void* base = nullptr;
+    HIP_TRY(hipMalloc(&base, off));
+    char* b = static_cast<char*>(base);
+    w.base = base;
+    w.tok_cap = tcap;
+    w.b_cap = bcap;
+    w.X = (float*)(b + oX);
+    w.Y = (float*)(b + oY);
+    w.QKV = (float*)(b + oQKV);
+    w.CTX = (float*)(b + oCTX);
+    w.F = (float*)(b + oF);
+    w.ids = (int*)(b + oIds);
+    w.mask = (int*)(b + oMask);
+    w.counts = (int*)(b + oCounts);
+    w.cu = (int*)(b + oCu);
+    w.ntok = (int*)(b + oNtok);
+    w.tok_id = (int*)(b + oTid);
+    w.tok_pos = (int*)(b + oTpos);
+    w.err = (int*)(b + oErr);
+    w.out = (float*)(b + oOut);
+    HIP_TRY(hipMemset(w.err, 0, 4));
+    return EBH_OK;
+}
+
+int ensure_host_staging(ebh_model* m, int64_t T, int64_t outn) {
+    if (T > m->h_cap) {
+        if (m->h_ids) (void)hipHostFree(m->h_ids);
+        if (m->h_mask) (void)hipHostFree(m->h_mask);
+        m->h_ids = m->h_mask = nullptr;
+        m->h_cap = 0;
+        HIP_TRY(hipHostMalloc((void**)&m->h_ids, std::max<int64_t>(T, 1) * 4, hipHostMallocDefault));
+        HIP_TRY(hipHostMalloc((void**)&m->h_mask, std::max<int64_t>(T, 1) * 4, hipHostMallocDefault));
+        m->h_cap = T;
+    }
+    if (outn > m->h_out_cap) {
+        if (m->h_out) (void)hipHostFree(m->h_out);
+        m->h_out = nullptr;
+        m->h_out_cap = 0;
+        HIP_TRY(hipHostMalloc((void**)&m->h_out, std::max<int64_t>(outn, 1) * 4, hipHostMallocDefault));
+        m->h_out_cap = outn;
+    }
+    if (!m->h_err) HIP_TRY(hipHostMalloc((void**)&m->h_err, 4, hipHostMallocDefault));
+    return EBH_OK;
+}
+
+// Enqueue the whole forward on stream s (ids/mask already in device memory).
+int enqueue_forward(ebh_model* m, const int* d_ids, const int* d_mask, int B, int S,
+                    int normalize, float* d_out, hipStream_t s) {
+    const ebh_config& c = m->cfg;
+    const int H = c.hidden_size, I = c.intermediate_size, nh = c.num_attention_heads;
+    const int hd = H / nh;
+    const float eps = c.layer_norm_eps;
+    const float scale = 1.0f / sqrtf((float)hd);  // src/lib.rs:196-197
+    Workspace& w = m->ws;
+    const int T = B * S;
+    if (m->has_done) HIP_TRY(hipStreamWaitEvent(s, m->done, 0));
+
+    ProfPair pp{};
+    bool on = false;
+    HIP_TRY(ebh::launch_pack(d_ids, d_mask, B, S, w.counts, w.cu, w.ntok, w.tok_id, w.tok_pos,
+                             w.err, s));
+    prof_begin(m, EBH_PROF_EMBED, s, pp, on);
+    HIP_TRY(ebh::launch_embed_ln(w.tok_id, w.tok_pos, w.ntok, T, m->word, m->pos, m->type0,
+                                 m->emb_g, m->emb_b, c.vocab_size, H, eps, w.X, w.err, s));
+    prof_end(m, s, pp, on);
+
+    const bool bf16 = m->dtype == EBH_DTYPE_BF16;
+    auto gemm = [&](int kind, const float* A, const float* W32, const uint16_t* W16,
+                    const float* bias, const float* R, float* C, int N, int K, int epi) -> int {
+        ebh::GemmArgs a{};
+        a.A = A;
+        a.W = bf16 ? (const void*)W16 : (const void*)W32;
+        a.bias = bias;
+        a.R = R;
+        a.C = C;
+        a.lda = K;
+        a.ldw = K;
+        a.ldr = N;
+        a.ldc = N;
+        a.M_max = T;
+        a.M_dev = w.ntok;
+        a.N = N;
+        a.K = K;
+        ProfPair p2{};
+        bool on2 = false;
+        prof_begin(m, kind, s, p2, on2);
+        hipError_t e = bf16 ? ebh::launch_gemm_bf16(a, epi, s) : ebh::launch_gemm_f32(a, epi, s);
+        prof_end(m, s, p2, on2);
+        if (e != hipSuccess) return fail(EBH_ERR_HIP, "gemm launch failed: %s", hipGetErrorString(e));
+        return EBH_OK;
+    };
+
+    for (const DevLayer& L : m->layers) {
+        int rc;
+        if ((rc = gemm(EBH_PROF_GEMM_QKV, w.X, L.wqkv, L.wqkv16, L.bqkv, nullptr, w.QKV, 3 * H, H,
+                       ebh::EPI_BIAS)))
+            return rc;
+        prof_begin(m, EBH_PROF_ATTENTION, s, pp, on);
+        HIP_TRY(ebh::launch_attention(w.QKV, w.cu, B, S, H, nh, hd, scale, w.CTX, s));
+        prof_end(m, s, pp, on);
+        if ((rc = gemm(EBH_PROF_GEMM_OUT, w.CTX, L.wo, L.wo16, L.bo, w.X, w.Y, H, H,
+                       ebh::EPI_BIAS_RESID)))
+            return rc;
+        prof_begin(m, EBH_PROF_LAYERNORM, s, pp, on);
+        HIP_TRY(ebh::launch_layernorm(w.Y, w.X, L.ln1_g, L.ln1_b, T, w.ntok, H, eps, s));
+        prof_end(m, s, pp, on);
+        if ((rc = gemm(EBH_PROF_GEMM_FFN_UP, w.X, L.w1, L.w116, L.b1, nullptr, w.F, I, H,
+                       ebh::EPI_BIAS_GELU)))
+            return rc;
+        if ((rc = gemm(EBH_PROF_GEMM_FFN_DOWN, w.F, L.w2, L.w216, L.b2, w.X, w.Y, H, I,
+                       ebh::EPI_BIAS_RESID)))
+            return rc;
+        prof_begin(m, EBH_PROF_LAYERNORM, s, pp, on);
+        HIP_TRY(ebh::launch_layernorm(w.Y, w.X, L.ln2_g, L.ln2_b, T, w.ntok, H, eps, s));
+        prof_end(m, s, pp, on);
+    }
+    prof_begin(m, EBH_PROF_POOL, s, pp, on);
+    HIP_TRY(ebh::launch_pool(w.X, w.cu, B, H, S, normalize, d_out, s));
+    prof_end(m, s, pp, on);
+    HIP_TRY(hipEventRecord(m->done, s));
+    m->has_done = true;
+    m->last_B = B;
+    return EBH_OK;
+}
+
+// Blocking forward from int32 host ids/mask already validated into h_ids/h_mask.
+int forward_host_staged(ebh_model* m, int B, int S, int normalize, float* out) {
+    const int64_t T = (int64_t)B * S;
+    const int H = m->cfg.hidden_size;
+    hipStream_t s = m->stream;
+    int rc = ensure_workspace(m, B, S);
+    if (rc) return rc;
+    if (m->has_done) HIP_TRY(hipStreamWaitEvent(s, m->done, 0));
+    HIP_TRY(hipMemcpyAsync(m->ws.ids, m->h_ids, T * 4, hipMemcpyHostToDevice, s));
+    HIP_TRY(hipMemcpyAsync(m->ws.mask, m->h_mask, T * 4, hipMemcpyHostToDevice, s));
+    if ((rc = enqueue_forward(m, m->ws.ids, m->ws.mask, B, S, normalize, m->ws.out, s))) return rc;
+    HIP_TRY(hipMemcpyAsync(m->h_out, m->ws.out, (size_t)B * H * 4, hipMemcpyDeviceToHost, s));
+    HIP_TRY(hipMemcpyAsync(m->h_err, m->ws.err, 4, hipMemcpyDeviceToHost, s));
+    HIP_TRY(hipStreamSynchronize(s));
+    if (*m->h_err) return fail(EBH_ERR_RANGE, "token id out of range for vocab %d", m->cfg.vocab_size);
+    memcpy(out, m->h_out, (size_t)B * H * 4);
+    return EBH_OK;
+}
+
+int check_model_ready(const ebh_model* m) {
+    if (!m) return fail(EBH_ERR_INVALID_ARG, "null model");
+    if (!m->finalized) return fail(EBH_ERR_STATE, "model is not finalized (call ebh_finalize)");
+    return EBH_OK;
+}
+
+int check_dims(const ebh_model* m, int B, int S) {
+    if (B < 0 || S < 0) return fail(EBH_ERR_INVALID_ARG, "negative batch or sequence length");
+    if (S > m->cfg.max_position_embeddings)
+        return fail(EBH_ERR_RANGE, "sequence length %d exceeds max_position_embeddings %d", S,
+                    m->cfg.max_position_embeddings);
+    if ((int64_t)B * S > (int64_t)1 << 30)
+        return fail(EBH_ERR_INVALID_ARG, "batch*seq %lld too large", (long long)B * S);
+    return EBH_OK;
+}
+
+}  // namespace
+
+// ===========================================================================
+// C ABI
+// ===========================================================================
+extern "C" {
+
+const char* ebh_last_error(void) { return g_err.c_str(); }
+
+int ebh_create(const ebh_config* cfg, ebh_model** out) {
+    if (!cfg || !out) return fail(EBH_ERR_INVALID_ARG, "null argument");
+    *out = nullptr;
+    int rc = check_config(*cfg);
+    if (rc) return rc;
+    ebh_model* m = new ebh_model();
+    m->cfg = *cfg;
+    *out = m;
+    return EBH_OK;
+}
+
+int ebh_set_tensor(ebh_model* m, const char* name, const float* data, const int64_t* shape,
+                   int32_t ndim) {
+    if (!m || !name || !shape || (!data && ndim > 0)) return fail(EBH_ERR_INVALID_ARG, "null argument");
+    if (m->finalized) return fail(EBH_ERR_STATE, "model already finalized");
+    std::vector<int64_t> storage;
+    const std::vector<int64_t>* exp = expected_shape(m->cfg, name, storage);
+    if (!exp) return fail(EBH_ERR_NOT_FOUND, "unknown tensor %s", name);
+    if (exp->size() == 1 && ndim != 1)
+        return fail(EBH_ERR_SHAPE, "Expected 1D tensor, got shape %s for %s",
+                    shape_str(shape, ndim).c_str(), name);
+    if ((int)exp->size() != ndim || !std::equal(exp->begin(), exp->end(), shape))
+        return fail(EBH_ERR_SHAPE, "Shape error: %s has shape %s, expected %s", name,
+                    shape_str(shape, ndim).c_str(), shape_str(exp->data(), (int)exp->size()).c_str());
+    int64_t n = 1;
+    for (int i = 0; i < ndim; ++i) n *= shape[i];
+    HostTensor& t = m->host[name];
+    t.shape.assign(shape, shape + ndim);
+    t.data.assign(data, data + n);
+    return EBH_OK;
+}
+
+int ebh_finalize(ebh_model* m, int32_t dtype) {
+    if (!m) return fail(EBH_ERR_INVALID_ARG, "null model");
+    std::lock_guard<std::mutex> lk(m->mu);
+    if (m->finalized) return fail(EBH_ERR_STATE, "model already finalized");
+    if (dtype != EBH_DTYPE_F32 && dtype != EBH_DTYPE_BF16)
+        return fail(EBH_ERR_INVALID_ARG, "unknown dtype %d", dtype);
+    const auto names = expected_tensors(m->cfg);
+    for (auto& kv : names)
+        if (!m->host.count(kv.first)) return fail(EBH_ERR_NOT_FOUND, "Tensor %s not found", kv.first.c_str());
+
+    const ebh_config& c = m->cfg;
+    const size_t H = c.hidden_size, I = c.intermediate_size, L = c.num_hidden_layers;
+    // Layout of the single device weight block.
+    size_t off = 0;
+    auto take = [&](size_t bytes) { size_t o = off; off += align_up(bytes); return o; };
+    struct Off { size_t wqkv, bqkv, wo, bo, ln1_g, ln1_b, w1, b1, w2, b2, ln2_g, ln2_b, wqkv16, wo16, w116, w216; };
+    const size_t oWord = take((size_t)c.vocab_size * H * 4), oPos = take((size_t)c.max_position_embeddings * H * 4),
+                 oType = take(H * 4), oEg = take(H * 4), oEb = take(H * 4);
+    std::vector<Off> lo(L);
+    for (size_t l = 0; l < L; ++l) {
+        Off& o = lo[l];
+        o.wqkv = take(3 * H * H * 4); o.bqkv = take(3 * H * 4);
+        o.wo = take(H * H * 4); o.bo = take(H * 4);
+        o.ln1_g = take(H * 4); o.ln1_b = take(H * 4);
+        o.w1 = take(I * H * 4); o.b1 = take(I * 4);
+        o.w2 = take(H * I * 4); o.b2 = take(H * 4);
+        o.ln2_g = take(H * 4); o.ln2_b = take(H * 4);
+    }
+    const size_t f32_bytes = off;
+    if (dtype == EBH_DTYPE_BF16)
+        for (size_t l = 0; l < L; ++l) {
+            Off& o = lo[l];
+            o.wqkv16 = take(3 * H * H * 2); o.wo16 = take(H * H * 2);
+            o.w116 = take(I * H * 2); o.w216 = take(H * I * 2);
+        }
+
+    std::vector<char> stage(f32_bytes, 0);
+    auto put = [&](size_t o, const std::string& name, size_t row_off = 0) {
+        const HostTensor& t = m->host.at(name);
+        memcpy(stage.data() + o + row_off, t.data.data(), t.data.size() * 4);
+    };
+    put(oWord, "embeddings.word_embeddings.weight");
+    put(oPos, "embeddings.position_embeddings.weight");
+    {   // token type row 0 only (src/lib.rs:658)
+        const HostTensor& t = m->host.at("embeddings.token_type_embeddings.weight");
+        memcpy(stage.data() + oType, t.data.data(), H * 4);
+    }
+    put(oEg, "embeddings.LayerNorm.weight");
+    put(oEb, "embeddings.LayerNorm.bias");
+    for (size_t l = 0; l < L; ++l) {
+        const std::string p = "encoder.layer." + std::to_string(l) + ".";
+        const Off& o = lo[l];
+        put(o.wqkv, p + "attention.self.query.weight", 0);
+        put(o.wqkv, p + "attention.self.key.weight", H * H * 4);
+        put(o.wqkv, p + "attention.self.value.weight", 2 * H * H * 4);
+        put(o.bqkv, p + "attention.self.query.bias", 0);
+        put(o.bqkv, p + "attention.self.key.bias", H * 4);
+        put(o.bqkv, p + "attention.self.value.bias", 2 * H * 4);
+        put(o.wo, p + "attention.output.dense.weight");
+        put(o.bo, p + "attention.output.dense.bias");
+        put(o.ln1_g, p + "attention.output.LayerNorm.weight");
+        put(o.ln1_b, p + "attention.output.LayerNorm.bias");
+        put(o.w1, p + "intermediate.dense.weight");
+        put(o.b1, p + "intermediate.dense.bias");
+        put(o.w2, p + "output.dense.weight");
+        put(o.b2, p + "output.dense.bias");
+        put(o.ln2_g, p + "output.LayerNorm.weight");
+        put(o.ln2_b, p + "output.LayerNorm.bias");
+    }
+
+    HIP_TRY(hipGetDevice(&m->device));
+    HIP_TRY(hipStreamCreateWithFlags(&m->stream, hipStreamNonBlocking));
+    HIP_TRY(hipEventCreateWithFlags(&m->done, hipEventDisableTiming));
+    HIP_TRY(hipMalloc(&m->wbase, off));
+    HIP_TRY(hipMemcpy(m->wbase, stage.data(), f32_bytes, hipMemcpyHostToDevice));
+    char* b = static_cast<char*>(m->wbase);
+    m->word = (float*)(b + oWord);
+    m->pos = (float*)(b + oPos);
+    m->type0 = (float*)(b + oType);
+    m->emb_g = (float*)(b + oEg);
+    m->emb_b = (float*)(b + oEb);
+    m->layers.resize(L);
+    for (size_t l = 0; l < L; ++l) {
+        const Off& o = lo[l];
+        DevLayer& d = m->layers[l];
+        d.wqkv = (float*)(b + o.wqkv); d.bqkv = (float*)(b + o.bqkv);
+        d.wo = (float*)(b + o.wo); d.bo = (float*)(b + o.bo);
+        d.ln1_g = (float*)(b + o.ln1_g); d.ln1_b = (float*)(b + o.ln1_b);
+        d.w1 = (float*)(b + o.w1); d.b1 = (float*)(b + o.b1);
+        d.w2 = (float*)(b + o.w2); d.b2 = (float*)(b + o.b2);
+        d.ln2_g = (float*)(b + o.ln2_g); d.ln2_b = (float*)(b + o.ln2_b);
+        d.wqkv16 = d.wo16 = d.w116 = d.w216 = nullptr;
+        if (dtype == EBH_DTYPE_BF16) {
+            d.wqkv16 = (uint16_t*)(b + o.wqkv16); d.wo16 = (uint16_t*)(b + o.wo16);
+            d.w116 = (uint16_t*)(b + o.w116); d.w216 = (uint16_t*)(b + o.w216);
+            HIP_TRY(ebh::launch_f32_to_bf16(d.wqkv, d.wqkv16, (int64_t)(3 * H * H), m->stream));
+            HIP_TRY(ebh::launch_f32_to_bf16(d.wo, d.wo16, (int64_t)(H * H), m->stream));
+            HIP_TRY(ebh::launch_f32_to_bf16(d.w1, d.w116, (int64_t)(I * H), m->stream));
+            HIP_TRY(ebh::launch_f32_to_bf16(d.w2, d.w216, (int64_t)(H * I), m->stream));
+        }
+    }
+    HIP_TRY(hipStreamSynchronize(m->stream));
+    m->dtype = dtype;
+    m->finalized = true;
+    m->host.clear();  // weights now live in HBM only
+    return EBH_OK;
+}
+
+void ebh_destroy(ebh_model* m) {
+    if (!m) return;
+    if (m->finalized) {
+        (void)hipSetDevice(m->device);
+        if (m->stream) (void)hipStreamSynchronize(m->stream);
+        for (auto& p : m->prof_events) { (void)hipEventDestroy(p.a); (void)hipEventDestroy(p.b); }
+        for (auto& e : m->prof_free) (void)hipEventDestroy(e);
+        if (m->ws.base) (void)hipFree(m->ws.base);
+        if (m->wbase) (void)hipFree(m->wbase);
+        if (m->h_ids) (void)hipHostFree(m->h_ids);
+        if (m->h_mask) (void)hipHostFree(m->h_mask);
+        if (m->h_out) (void)hipHostFree(m->h_out);
+        if (m->h_err) (void)hipHostFree(m->h_err);
+        if (m->done) (void)hipEventDestroy(m->done);
+        if (m->stream) (void)hipStreamDestroy(m->stream);
+    }
+    delete m;
+}
+
+int ebh_forward(ebh_model* m, const float* input_ids, const float* attention_mask, int32_t B,
+                int32_t S, float* out) {
+    int rc = check_model_ready(m);
+    if (rc) return rc;
+    if ((rc = check_dims(m, B, S))) return rc;
+    if (B == 0) return EBH_OK;  // src/lib.rs:480-482
+    if (!input_ids || !attention_mask || !out) return fail(EBH_ERR_INVALID_ARG, "null buffer");
+    const int H = m->cfg.hidden_size;
+    if (S == 0) {  // mean over an empty sequence: zeros (count clamps to 1)
+        memset(out, 0, sizeof(float) * (size_t)B * H);
+        return EBH_OK;
+    }
+    std::lock_guard<std::mutex> lk(m->mu);
+    HIP_TRY(hipSetDevice(m->device));
+    const int64_t T = (int64_t)B * S;
+    if ((rc = ensure_host_staging(m, T, (int64_t)B * H))) return rc;
+    for (int64_t i = 0; i < T; ++i) {
+        // `token_id as usize` (src/lib.rs:639): truncation; NaN / negatives -> 0.
+        const float f = input_ids[i];
+        int64_t id = (f > 0.0f) ? (f >= 9.2e18f ? INT64_MAX : (int64_t)f) : 0;
+        if (id >= m->cfg.vocab_size)
+            return fail(EBH_ERR_RANGE, "token id %lld at [%lld, %lld] out of range for vocab %d",
+                        (long long)id, (long long)(i / S), (long long)(i % S), m->cfg.vocab_size);
+        const float mk = attention_mask[i];
+        if (mk != 0.0f && mk != 1.0f)
+            return fail(EBH_ERR_INVALID_ARG, "attention mask value %g at [%lld, %lld] is not 0 or 1",
+                        (double)mk, (long long)(i / S), (long long)(i % S));
+        m->h_ids[i] = (int)id;
+        m->h_mask[i] = mk != 0.0f;
+    }
+    return forward_host_staged(m, B, S, 0, out);
+}
+
+int ebh_encode(ebh_model* m, const uint32_t* ids, const uint32_t* mask, int32_t B, int32_t S,
+               int32_t normalize, float* out) {
+    int rc = check_model_ready(m);
+    if (rc) return rc;
+    if ((rc = check_dims(m, B, S))) return rc;
+    if (B == 0) return EBH_OK;
+    if (!ids || !mask || !out) return fail(EBH_ERR_INVALID_ARG, "null buffer");
+    const int H = m->cfg.hidden_size;
+    if (S == 0) {
+        memset(out, 0, sizeof(float) * (size_t)B * H);
+        return EBH_OK;
+    }
+    std::lock_guard<std::mutex> lk(m->mu);
+    HIP_TRY(hipSetDevice(m->device));
+    const int64_t T = (int64_t)B * S;
+    if ((rc = ensure_host_staging(m, T, (int64_t)B * H))) return rc;
+    for (int64_t i = 0; i < T; ++i) {
+        if (ids[i] >= (uint32_t)m->cfg.vocab_size)
+            return fail(EBH_ERR_RANGE, "token id %u at [%lld, %lld] out of range for vocab %d",
+                        ids[i], (long long)(i / S), (long long)(i % S), m->cfg.vocab_size);
+        if (mask[i] > 1)
+            return fail(EBH_ERR_INVALID_ARG, "attention mask value %u at [%lld, %lld] is not 0 or 1",
+                        mask[i], (long long)(i / S), (long long)(i % S));
+        m->h_ids[i] = (int)ids[i];
+        m->h_mask[i] = (int)mask[i];
+    }
+    return forward_host_staged(m, B, S, normalize ? 1 : 0, out);
+}
+
+int ebh_encode_device(ebh_model* m, const int32_t* ids, const int32_t* mask, int32_t B,
+                      int32_t S, int32_t normalize, float* out, void* stream) {
+    int rc = check_model_ready(m);
+    if (rc) return rc;
+    if ((rc = check_dims(m, B, S))) return rc;
+    if (B == 0) return EBH_OK;
+    if (!ids || !mask || !out) return fail(EBH_ERR_INVALID_ARG, "null buffer");
+    std::lock_guard<std::mutex> lk(m->mu);
+    HIP_TRY(hipSetDevice(m->device));
+    hipStream_t s = stream ? static_cast<hipStream_t>(stream) : m->stream;
+    if (S == 0) {
+        if (m->has_done) HIP_TRY(hipStreamWaitEvent(s, m->done, 0));
+        HIP_TRY(hipMemsetAsync(out, 0, sizeof(float) * (size_t)B * m->cfg.hidden_size, s));
+        return EBH_OK;
+    }
+    if ((rc = ensure_workspace(m, B, S))) return rc;
+    return enqueue_forward(m, ids, mask, B, S, normalize ? 1 : 0, out, s);
+}
+
+int ebh_synchronize(ebh_model* m) {
+    int rc = check_model_ready(m);
+    if (rc) return rc;
+    std::lock_guard<std::mutex> lk(m->mu);
+    HIP_TRY(hipSetDevice(m->device));
+    if (m->has_done) HIP_TRY(hipEventSynchronize(m->done));
+    if (!m->ws.base) return EBH_OK;
+    int err = 0;
+    HIP_TRY(hipMemcpy(&err, m->ws.err, 4, hipMemcpyDeviceToHost));
+    if (err) {
+        HIP_TRY(hipMemset(m->ws.err, 0, 4));
+        return fail(EBH_ERR_RANGE, "token id out of range for vocab %d", m->cfg.vocab_size);
+    }
+    return EBH_OK;
+}
+
+int ebh_last_tokens(ebh_model* m, int32_t* tok_ids, int32_t* tok_pos, int64_t tok_capacity,
+                    int32_t* cu_seqlens, int64_t cu_capacity, int32_t* n_tokens) {
+    int rc = check_model_ready(m);
+    if (rc) return rc;
+    std::lock_guard<std::mutex> lk(m->mu);
+    HIP_TRY(hipSetDevice(m->device));
+    if (!m->ws.base || !m->has_done) return fail(EBH_ERR_STATE, "no forward has run");
+    HIP_TRY(hipEventSynchronize(m->done));
+    int n = 0;
+    HIP_TRY(hipMemcpy(&n, m->ws.ntok, 4, hipMemcpyDeviceToHost));
+    if (n_tokens) *n_tokens = n;
+    if ((tok_ids || tok_pos) && tok_capacity < n)
+        return fail(EBH_ERR_INVALID_ARG, "token capacity %lld < %d", (long long)tok_capacity, n);
+    if (tok_ids) HIP_TRY(hipMemcpy(tok_ids, m->ws.tok_id, (size_t)n * 4, hipMemcpyDeviceToHost));
+    if (tok_pos) HIP_TRY(hipMemcpy(tok_pos, m->ws.tok_pos, (size_t)n * 4, hipMemcpyDeviceToHost));
+    if (cu_seqlens) {
+        if (cu_capacity < m->last_B + 1)
+            return fail(EBH_ERR_INVALID_ARG, "cu_seqlens capacity %lld < %d", (long long)cu_capacity, m->last_B + 1);
+        HIP_TRY(hipMemcpy(cu_seqlens, m->ws.cu, (size_t)(m->last_B + 1) * 4, hipMemcpyDeviceToHost));
+    }
+    return EBH_OK;
+}
+
+int ebh_model_info(const ebh_model* m, ebh_config* cfg_out, int32_t* dtype_out) {
+    if (!m) return fail(EBH_ERR_INVALID_ARG, "null model");
+    if (cfg_out) *cfg_out = m->cfg;
+    if (dtype_out) *dtype_out = m->dtype;
+    return EBH_OK;
+}
+
+int ebh_profile_enable(ebh_model* m, int32_t kernel) {
+    int rc = check_model_ready(m);
+    if (rc) return rc;
+    if (kernel < EBH_PROF_NONE || kernel > EBH_PROF_POOL)
+        return fail(EBH_ERR_INVALID_ARG, "unknown kernel id %d", kernel);
+    std::lock_guard<std::mutex> lk(m->mu);
+    HIP_TRY(hipSetDevice(m->device));
+    if (m->has_done) HIP_TRY(hipEventSynchronize(m->done));
+    for (auto& p : m->prof_events) { m->prof_free.push_back(p.a); m->prof_free.push_back(p.b); }
+    m->prof_events.clear();
+    m->prof_kind = kernel;
+    return EBH_OK;
+}
+
+int ebh_profile_read(ebh_model* m, int64_t* launches, double* total_ms) {
+    int rc = check_model_ready(m);
+    if (rc) return rc;
+    std::lock_guard<std::mutex> lk(m->mu);
+    HIP_TRY(hipSetDevice(m->device));
+    double tot = 0.0;
+    for (auto& p : m->prof_events) {
+        HIP_TRY(hipEventSynchronize(p.b));
+        float ms = 0.0f;
+        HIP_TRY(hipEventElapsedTime(&ms, p.a, p.b));
+        tot += ms;
+    }
+    if (launches) *launches = (int64_t)m->prof_events.size();
+    if (total_ms) *total_ms = tot;
+    return EBH_OK;
+}
+
+// ---------------------------------------------------------------------------
+// op-level entry points (edgebert_hip_ops.h)
+// ---------------------------------------------------------------------------
+int ebh_op_gemm(const float* A, int64_t lda, const void* W, int64_t ldw, int32_t w_dtype,
+                const float* bias, const float* residual, int64_t ldr, float* C, int64_t ldc,
+                int32_t M, int32_t N, int32_t K, int32_t epilogue, void* stream) {
+    if (!A || !W || !bias || !C) return fail(EBH_ERR_INVALID_ARG, "null buffer");
+    if (M < 0 || N <= 0 || K <= 0) return fail(EBH_ERR_INVALID_ARG, "bad GEMM shape");
+    if (epilogue < EBH_EPI_BIAS || epilogue > EBH_EPI_BIAS_RESID)
+        return fail(EBH_ERR_INVALID_ARG, "unknown epilogue %d", epilogue);
+    if (epilogue == EBH_EPI_BIAS_RESID && (!residual || ldr < N))
+        return fail(EBH_ERR_INVALID_ARG, "residual epilogue needs a residual of row stride >= N");
+    const int q = w_dtype == EBH_DTYPE_BF16 ? 8 : 4;
+    if (w_dtype != EBH_DTYPE_F32 && w_dtype != EBH_DTYPE_BF16)
+        return fail(EBH_ERR_INVALID_ARG, "unknown dtype %d", w_dtype);
+    if (K % q || lda % 4 || ldw % q || lda < K || ldw < K || ldc < N)
+        return fail(EBH_ERR_INVALID_ARG, "K and strides must be multiples of %d and cover the rows", q);
+    if (M == 0) return EBH_OK;
+    ebh::GemmArgs a{};
+    a.A = A; a.W = W; a.bias = bias; a.R = residual; a.C = C;
+    a.lda = lda; a.ldw = ldw; a.ldr = ldr; a.ldc = ldc;
+    a.M_max = M; a.M_dev = nullptr; a.N = N; a.K = K;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    hipError_t e = w_dtype == EBH_DTYPE_BF16 ? ebh::launch_gemm_bf16(a, epilogue, s)
+                                              : ebh::launch_gemm_f32(a, epilogue, s);
+    if (e != hipSuccess) return fail(EBH_ERR_HIP, "gemm launch failed: %s", hipGetErrorString(e));
+    return EBH_OK;
+}
+
+int ebh_op_attention(const float* qkv, const int32_t* cu_seqlens, int32_t B, int32_t max_len,
+                     int32_t hidden, int32_t num_heads, float* ctx, void* stream) {
+    if (!qkv || !cu_seqlens || !ctx) return fail(EBH_ERR_INVALID_ARG, "null buffer");
+    if (B < 0 || max_len < 0 || hidden <= 0 || num_heads <= 0 || hidden % num_heads)
+        return fail(EBH_ERR_INVALID_ARG, "bad attention shape");
+    const int hd = hidden / num_heads;
+    if (hd != 32 && hd != 64) return fail(EBH_ERR_INVALID_ARG, "head_dim %d unsupported", hd);
+    const float scale = 1.0f / sqrtf((float)hd);
+    HIP_TRY(ebh::launch_attention(qkv, cu_seqlens, B, max_len, hidden, num_heads, hd, scale, ctx,
+                                  static_cast<hipStream_t>(stream)));
+    return EBH_OK;
+}
+
+int ebh_op_layer_norm(const float* x, const float* gamma, const float* beta, int32_t rows,
+                      int32_t H, float eps, float* y, void* stream) {
+    if (!x || !gamma || !beta || !y) return fail(EBH_ERR_INVALID_ARG, "null buffer");
+    if (rows < 0 || H <= 0 || H > 2048) return fail(EBH_ERR_INVALID_ARG, "bad LayerNorm shape");
+    HIP_TRY(ebh::launch_layernorm(x, y, gamma, beta, rows, nullptr, H, eps,
+                                  static_cast<hipStream_t>(stream)));
+    return EBH_OK;
+}
+
+int ebh_op_pool(const float* x, const int32_t* cu_seqlens, int32_t B, int32_t H, int32_t S,
+                int32_t normalize, float* out, void* stream) {
+    if (!x || !cu_seqlens || !out) return fail(EBH_ERR_INVALID_ARG, "null buffer");
+    if (B < 0 || H <= 0 || H > 2048 || S < 0) return fail(EBH_ERR_INVALID_ARG, "bad pool shape");
+    HIP_TRY(ebh::launch_pool(x, cu_seqlens, B, H, S, normalize ? 1 : 0, out,
+                             static_cast<hipStream_t>(stream)));
+    return EBH_OK;
+}
+
+int ebh_op_pack(const int32_t* ids, const int32_t* mask, int32_t B, int32_t S, int32_t* counts,
+                int32_t* cu_seqlens, int32_t* n_tokens, int32_t* tok_id, int32_t* tok_pos,
+                int32_t* err, void* stream) {
+    if (!ids || !mask || !counts || !cu_seqlens || !n_tokens || !tok_id || !tok_pos || !err)
+        return fail(EBH_ERR_INVALID_ARG, "null buffer");
+    if (B < 0 || S < 0) return fail(EBH_ERR_INVALID_ARG, "bad pack shape");
+    HIP_TRY(ebh::launch_pack(ids, mask, B, S, counts, cu_seqlens, n_tokens, tok_id, tok_pos, err,
+                             static_cast<hipStream_t>(stream)));
+    return EBH_OK;
+}
+
+int ebh_op_embed_ln(const int32_t* tok_id, const int32_t* tok_pos, const int32_t* n_tokens,
+                    int32_t T_max, const float* word, const float* pos, const float* type0,
+                    const float* gamma, const float* beta, int32_t V, int32_t H, float eps,
+                    float* x, int32_t* err, void* stream) {
+    if (!tok_id || !tok_pos || !n_tokens || !word || !pos || !type0 || !gamma || !beta || !x || !err)
+        return fail(EBH_ERR_INVALID_ARG, "null buffer");
+    if (T_max < 0 || V <= 0 || H <= 0 || H > 2048) return fail(EBH_ERR_INVALID_ARG, "bad embed shape");
+    HIP_TRY(ebh::launch_embed_ln(tok_id, tok_pos, n_tokens, T_max, word, pos, type0, gamma, beta,
+                                 V, H, eps, x, err, static_cast<hipStream_t>(stream)));
+    return EBH_OK;
+}
+
+int ebh_op_f32_to_bf16(const float* x, uint16_t* y, int64_t n, void* stream) {
+    if (!x || !y || n < 0) return fail(EBH_ERR_INVALID_ARG, "bad conversion arguments");
+    HIP_TRY(ebh::launch_f32_to_bf16(x, y, n, static_cast<hipStream_t>(stream)));
+    return EBH_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,91 @@
+// kernels.hpp -- device helpers and kernel launchers of the gfx950 encoder path.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace ebh {
+
+// GEMM epilogues: bias is always added; then optionally GELU (FFN up) or a
+// residual add (attention output and FFN down projections).
+enum Epilogue : int { EPI_BIAS = 0, EPI_BIAS_GELU = 1, EPI_BIAS_RESID = 2 };
+
+struct GemmArgs {
+    const void* A;       // [M, K] row-major activations (fp32)
+    const void* W;       // [N, K] row-major weights (fp32 or bf16)
+    const float* bias;   // [N]
+    const float* R;      // [M, N] residual (EPI_BIAS_RESID) or nullptr
+    float* C;            // [M, N]
+    int64_t lda, ldw, ldr, ldc;
+    int M_max;           // grid is sized for this many rows
+    const int* M_dev;    // actual rows, read on device (nullptr: M_max)
+    int N, K;
+};
+
+// C = epi(A . W^T + bias); W fp32 (gemm_f32) or bf16 (gemm_bf16, A rounded to bf16).
+hipError_t launch_gemm_f32(const GemmArgs& a, int epi, hipStream_t s);
+hipError_t launch_gemm_bf16(const GemmArgs& a, int epi, hipStream_t s);
+
+// Masked multi-head attention over packed sequences: qkv [T, 3H] rows
+// (q | k | v), cu_seqlens [B+1]; ctx [T, H].  head_dim 32 or 64.
+hipError_t launch_attention(const float* qkv, const int* cu_seqlens, int B, int max_len,
+                            int H, int nh, int head_dim, float scale, float* ctx,
+                            hipStream_t s);
+
+// Row LayerNorm (population variance), y may alias x.
+hipError_t launch_layernorm(const float* x, float* y, const float* g, const float* b,
+                            int rows_max, const int* rows_dev, int H, float eps, hipStream_t s);
+
+// Token packing: mask [B,S] -> cu_seqlens [B+1], n_tokens, packed ids/positions.
+hipError_t launch_pack(const int* ids, const int* mask, int B, int S, int* counts, int* cu,
+                       int* n_tokens, int* tok_id, int* tok_pos, int* err, hipStream_t s);
+
+// Embedding gather + position + token type 0 + LayerNorm over packed tokens.
+hipError_t launch_embed_ln(const int* tok_id, const int* tok_pos, const int* n_tokens,
+                           int T_max, const float* word, const float* pos, const float* type0,
+                           const float* g, const float* b, int V, int H, float eps, float* x,
+                           int* err, hipStream_t s);
+
+// Masked mean over each packed sequence, optional L2 normalisation; out [B, H].
+hipError_t launch_pool(const float* x, const int* cu_seqlens, int B, int H, int S,
+                       int normalize, float* out, hipStream_t s);
+
+// fp32 -> bf16 (round to nearest even) for weight upload.
+hipError_t launch_f32_to_bf16(const float* x, uint16_t* y, int64_t n, hipStream_t s);
+
+// ---------------------------------------------------------------------------
+// device helpers
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+    return v;
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
+    return v;
+}
+
+// exp(x) = 2^(x * log2 e) on the hardware exp2 (v_exp_f32).
+__device__ __forceinline__ float fast_exp(float x) {
+    return __builtin_amdgcn_exp2f(x * 1.4426950408889634f);
+}
+
+// tanh-form GELU of the reference (src/lib.rs:958-978, constants 151-152).
+__device__ __forceinline__ float gelu_tanh(float val) {
+    const float SQRT_2_OVER_PI = 0.7978845608f;
+    const float GELU_COEFF = 0.044715f;
+    float val_cubed = val * val * val;
+    float inner = SQRT_2_OVER_PI * (val + GELU_COEFF * val_cubed);
+    return val * 0.5f * (1.0f + tanhf(inner));
+}
+
+__device__ __forceinline__ uint16_t f32_to_bf16_rne(float f) {
+    uint32_t u = __float_as_uint(f);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);  // quiet NaN
+    u += 0x7fffu + ((u >> 16) & 1u);
+    return (uint16_t)(u >> 16);
+}
+
+}  // namespace ebh

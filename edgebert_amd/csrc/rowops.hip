@@ -1,0 +1,286 @@
+// rowops.hip -- HBM-bound row kernels of the encoder path: token packing,
+// embedding gather + LayerNorm, LayerNorm, masked mean pool + L2 normalise.
+//
+// One wave64 owns one row of H floats (NC = ceil(H/64) values per lane,
+// element c*64 + lane so every load/store instruction covers 256 contiguous
+// bytes); mean and variance are two wave reductions over register-resident
+// values, so each row is read once and written once.
+#include "kernels.hpp"
+
+namespace ebh {
+
+// ---------------------------------------------------------------------------
+// Token packing.  The reference runs every padded position through the
+// encoder and only drops pads in the pooling (src/lib.rs:993-1010); a pad
+// never influences a real token (it is a masked key, and every other op is
+// row-wise), so only mask == 1 tokens are packed, keeping their original
+// positions for the position embedding.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void pack_count_kernel(const int* __restrict__ mask, int S,
+                                                         int* __restrict__ counts,
+                                                         int* __restrict__ err) {
+    __shared__ int part[4];
+    const int b = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    int n = 0;
+    for (int s0 = 0; s0 < S; s0 += 256) {
+        const int s = s0 + tid;
+        const bool on = s < S && mask[(int64_t)b * S + s] != 0;
+        const unsigned long long bal = __ballot(on);
+        n += __popcll(bal);
+    }
+    if (lane == 0) part[wave] = n;
+    __syncthreads();
+    if (tid == 0) {
+        counts[b] = part[0] + part[1] + part[2] + part[3];
+        if (b == 0) *err = 0;  // clear the id-range flag for this forward
+    }
+}
+
+// Exclusive scan of counts[0..B) -> cu[0..B], n_tokens = cu[B]; one workgroup.
+__global__ __launch_bounds__(1024) void pack_scan_kernel(const int* __restrict__ counts, int B,
+                                                         int* __restrict__ cu,
+                                                         int* __restrict__ n_tokens) {
+    __shared__ int buf[1024];
+    const int tid = threadIdx.x;
+    const int per = (B + 1023) / 1024;
+    const int lo = min(B, tid * per), hi = min(B, lo + per);
+    int local = 0;
+    for (int i = lo; i < hi; ++i) local += counts[i];
+    buf[tid] = local;
+    __syncthreads();
+    for (int off = 1; off < 1024; off <<= 1) {  // Hillis-Steele inclusive scan
+        const int v = tid >= off ? buf[tid - off] : 0;
+        __syncthreads();
+        buf[tid] += v;
+        __syncthreads();
+    }
+    int run = buf[tid] - local;  // exclusive prefix of this thread's segment
+    for (int i = lo; i < hi; ++i) {
+        cu[i] = run;
+        run += counts[i];
+    }
+    if (tid == 1023) {
+        cu[B] = buf[1023];
+        *n_tokens = buf[1023];
+    }
+}
+
+__global__ __launch_bounds__(256) void pack_scatter_kernel(const int* __restrict__ ids,
+                                                           const int* __restrict__ mask, int S,
+                                                           const int* __restrict__ cu,
+                                                           int* __restrict__ tok_id,
+                                                           int* __restrict__ tok_pos) {
+    __shared__ int part[4];
+    const int b = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    int base = cu[b];
+    for (int s0 = 0; s0 < S; s0 += 256) {
+        const int s = s0 + tid;
+        const bool on = s < S && mask[(int64_t)b * S + s] != 0;
+        const unsigned long long bal = __ballot(on);
+        if (lane == 0) part[wave] = __popcll(bal);
+        __syncthreads();
+        int before = 0;
+        for (int w = 0; w < wave; ++w) before += part[w];
+        const int total = part[0] + part[1] + part[2] + part[3];
+        const unsigned long long below = lane ? (bal & ((~0ull) >> (64 - lane))) : 0ull;
+        if (on) {
+            const int dst = base + before + __popcll(below);
+            tok_id[dst] = ids[(int64_t)b * S + s];
+            tok_pos[dst] = s;
+        }
+        base += total;
+        __syncthreads();
+    }
+}
+
+hipError_t launch_pack(const int* ids, const int* mask, int B, int S, int* counts, int* cu,
+                       int* n_tokens, int* tok_id, int* tok_pos, int* err, hipStream_t s) {
+    if (B <= 0) return hipSuccess;
+    hipLaunchKernelGGL(pack_count_kernel, dim3(B), dim3(256), 0, s, mask, S, counts, err);
+    hipLaunchKernelGGL(pack_scan_kernel, dim3(1), dim3(1024), 0, s, counts, B, cu, n_tokens);
+    hipLaunchKernelGGL(pack_scatter_kernel, dim3(B), dim3(256), 0, s, ids, mask, S, cu, tok_id,
+                       tok_pos);
+    return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
+// LayerNorm on a register-resident row (apply_layer_norm_3d, src/lib.rs:980-991):
+// mean, population variance, inv_std = 1/sqrt(var + eps),
+// y = (x - mean) * inv_std * gamma + beta.
+// ---------------------------------------------------------------------------
+template <int NC>
+__device__ __forceinline__ void ln_row(float (&v)[NC], int lane, int H, const float* g,
+                                       const float* b, float eps, float* y) {
+    float s = 0.0f;
+#pragma unroll
+    for (int c = 0; c < NC; ++c) s += v[c];
+    const float mean = wave_sum(s) / (float)H;
+    float ss = 0.0f;
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+        const int i = c * 64 + lane;
+        const float d = v[c] - mean;
+        if (i < H) ss += d * d;
+    }
+    const float var = wave_sum(ss) / (float)H;
+    const float inv_std = 1.0f / sqrtf(var + eps);
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+        const int i = c * 64 + lane;
+        if (i < H) y[i] = (v[c] - mean) * inv_std * g[i] + b[i];
+    }
+}
+
+template <int NC>
+__global__ __launch_bounds__(256) void layernorm_kernel(const float* x, float* y,
+                                                        const float* __restrict__ g,
+                                                        const float* __restrict__ bta,
+                                                        int rows_max, const int* rows_dev, int H,
+                                                        float eps) {
+    const int row = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+    const int rows = rows_dev ? *rows_dev : rows_max;
+    if (row >= rows) return;
+    const float* xr = x + (int64_t)row * H;
+    float v[NC];
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+        const int i = c * 64 + lane;
+        v[c] = i < H ? xr[i] : 0.0f;
+    }
+    ln_row<NC>(v, lane, H, g, bta, eps, y + (int64_t)row * H);
+}
+
+// Embeddings (Model::forward, src/lib.rs:628-661): word[id] + position[pos] +
+// token_type[0], then the embeddings LayerNorm.  An id outside [0, V) reads
+// row 0 and raises the error flag (the reference panics on such an id).
+template <int NC>
+__global__ __launch_bounds__(256) void embed_ln_kernel(
+    const int* __restrict__ tok_id, const int* __restrict__ tok_pos,
+    const int* __restrict__ n_tokens, const float* __restrict__ word,
+    const float* __restrict__ pos, const float* __restrict__ type0, const float* __restrict__ g,
+    const float* __restrict__ bta, int V, int H, float eps, float* __restrict__ x,
+    int* __restrict__ err) {
+    const int t = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+    if (t >= *n_tokens) return;
+    int id = tok_id[t];
+    if (id < 0 || id >= V) {
+        if (lane == 0) atomicOr(err, 1);
+        id = 0;
+    }
+    const float* wr = word + (int64_t)id * H;
+    const float* pr = pos + (int64_t)tok_pos[t] * H;
+    float v[NC];
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+        const int i = c * 64 + lane;
+        v[c] = i < H ? (wr[i] + pr[i]) + type0[i] : 0.0f;
+    }
+    ln_row<NC>(v, lane, H, g, bta, eps, x + (int64_t)t * H);
+}
+
+#define EBH_ROW_DISPATCH(KERNEL, H, GRID, STREAM, ...)                                       \
+    do {                                                                                     \
+        const int nc_ = ((H) + 63) / 64;                                                     \
+        if (nc_ <= 4) hipLaunchKernelGGL(KERNEL<4>, GRID, dim3(256), 0, STREAM, __VA_ARGS__);  \
+        else if (nc_ <= 6) hipLaunchKernelGGL(KERNEL<6>, GRID, dim3(256), 0, STREAM, __VA_ARGS__); \
+        else if (nc_ <= 8) hipLaunchKernelGGL(KERNEL<8>, GRID, dim3(256), 0, STREAM, __VA_ARGS__); \
+        else if (nc_ <= 12) hipLaunchKernelGGL(KERNEL<12>, GRID, dim3(256), 0, STREAM, __VA_ARGS__); \
+        else if (nc_ <= 16) hipLaunchKernelGGL(KERNEL<16>, GRID, dim3(256), 0, STREAM, __VA_ARGS__); \
+        else if (nc_ <= 32) hipLaunchKernelGGL(KERNEL<32>, GRID, dim3(256), 0, STREAM, __VA_ARGS__); \
+        else return hipErrorInvalidValue;                                                    \
+    } while (0)
+
+hipError_t launch_layernorm(const float* x, float* y, const float* g, const float* b,
+                            int rows_max, const int* rows_dev, int H, float eps, hipStream_t s) {
+    if (rows_max <= 0) return hipSuccess;
+    const dim3 grid((rows_max + 3) / 4);
+    EBH_ROW_DISPATCH(layernorm_kernel, H, grid, s, x, y, g, b, rows_max, rows_dev, H, eps);
+    return hipGetLastError();
+}
+
+hipError_t launch_embed_ln(const int* tok_id, const int* tok_pos, const int* n_tokens,
+                           int T_max, const float* word, const float* pos, const float* type0,
+                           const float* g, const float* b, int V, int H, float eps, float* x,
+                           int* err, hipStream_t s) {
+    if (T_max <= 0) return hipSuccess;
+    const dim3 grid((T_max + 3) / 4);
+    EBH_ROW_DISPATCH(embed_ln_kernel, H, grid, s, tok_id, tok_pos, n_tokens, word, pos, type0, g,
+                     b, V, H, eps, x, err);
+    return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
+// mean_pool (src/lib.rs:993-1010) + normalise (src/lib.rs:605-612): one
+// workgroup per sequence; the 4 waves sum interleaved tokens, then wave 0
+// combines, divides by max(count, 1) and optionally scales by
+// 1 / max(||x||, 1e-12).  A sequence with no real token among S > 0
+// positions is NaN, as the reference's all -inf softmax row makes it.
+// ---------------------------------------------------------------------------
+template <int NC>
+__global__ __launch_bounds__(256) void pool_kernel(const float* __restrict__ x,
+                                                   const int* __restrict__ cu, int H, int S,
+                                                   int normalize, float* __restrict__ out) {
+    __shared__ float red[3][NC * 64];
+    const int b = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int start = cu[b], len = cu[b + 1] - start;
+    float acc[NC];
+#pragma unroll
+    for (int c = 0; c < NC; ++c) acc[c] = 0.0f;
+    for (int t = wave; t < len; t += 4) {
+        const float* xr = x + (int64_t)(start + t) * H;
+#pragma unroll
+        for (int c = 0; c < NC; ++c) {
+            const int i = c * 64 + lane;
+            if (i < H) acc[c] += xr[i];
+        }
+    }
+    if (wave > 0) {
+#pragma unroll
+        for (int c = 0; c < NC; ++c) red[wave - 1][c * 64 + lane] = acc[c];
+    }
+    __syncthreads();
+    if (wave != 0) return;
+    const float count = fmaxf((float)len, 1.0f);
+    const bool all_masked = (len == 0 && S > 0);
+    float ss = 0.0f;
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+        const int i = c * 64 + lane;
+        float v = ((acc[c] + red[0][c * 64 + lane]) + red[1][c * 64 + lane]) + red[2][c * 64 + lane];
+        v = v / count;
+        if (all_masked) v = __builtin_nanf("");
+        acc[c] = v;
+        if (i < H) ss += v * v;
+    }
+    const float norm = normalize ? fmaxf(sqrtf(wave_sum(ss)), 1e-12f) : 1.0f;
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+        const int i = c * 64 + lane;
+        if (i < H) out[(int64_t)b * H + i] = normalize ? acc[c] / norm : acc[c];
+    }
+}
+
+hipError_t launch_pool(const float* x, const int* cu_seqlens, int B, int H, int S, int normalize,
+                       float* out, hipStream_t s) {
+    if (B <= 0) return hipSuccess;
+    EBH_ROW_DISPATCH(pool_kernel, H, dim3(B), s, x, cu_seqlens, H, S, normalize, out);
+    return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
+__global__ void f32_to_bf16_kernel(const float* __restrict__ x, uint16_t* __restrict__ y,
+                                   int64_t n) {
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+         i += (int64_t)gridDim.x * blockDim.x)
+        y[i] = f32_to_bf16_rne(x[i]);
+}
+
+hipError_t launch_f32_to_bf16(const float* x, uint16_t* y, int64_t n, hipStream_t s) {
+    if (n <= 0) return hipSuccess;
+    const int64_t blocks = (n + 255) / 256;
+    hipLaunchKernelGGL(f32_to_bf16_kernel, dim3((unsigned)(blocks < 65536 ? blocks : 65536)),
+                       dim3(256), 0, s, x, y, n);
+    return hipGetLastError();
+}
+
+}  // namespace ebh

@@ -1,0 +1,239 @@
+"""Host-side mirror of the reference ``Model`` (src/lib.rs:40-60, 155-666) over
+the gfx950 C ABI.
+
+Same entry points and meaning as the Rust API for this path:
+
+* ``Model.from_weights(weights, config)``   <- ``Model::from_weights`` (src/lib.rs:155)
+* ``Model.from_pretrained_path(dir)``       <- ``Model::from_pretrained_path`` (src/lib.rs:307)
+* ``Model.forward(input_ids, attention_mask)`` <- ``Model::forward`` (src/lib.rs:621):
+  f32 ``[B, S]`` ids / mask in, mean-pooled ``[B, H]`` out (not normalised)
+* ``Model.encode_ids(ids, mask, normalize)`` <- ``encode_uncached`` after
+  tokenisation (src/lib.rs:588-612)
+* ``Model.encode(texts, normalize)``          <- ``Model::encode`` (src/lib.rs:479-520),
+  including its 1000-entry LRU cache keyed ``"{text}||{normalize}"``; needs
+  the HF ``tokenizers`` Tokenizer the reference uses (``tokenizer.json``).
+
+Errors raise :class:`EbhError` carrying the C ABI's code and message.
+"""
+from __future__ import annotations
+
+import ctypes
+import json
+import os
+import threading
+from collections import OrderedDict
+
+import numpy as np
+
+from . import _native as N
+from .synth import BertConfig
+
+_DTYPES = {"fp32": N.EBH_DTYPE_F32, "f32": N.EBH_DTYPE_F32, "bf16": N.EBH_DTYPE_BF16}
+
+
+def _ptr(a: np.ndarray):
+    return ctypes.c_void_p(a.ctypes.data)
+
+
+def _cfg_struct(cfg: BertConfig) -> N.EbhConfig:
+    return N.EbhConfig(cfg.hidden_size, cfg.num_attention_heads, cfg.num_hidden_layers,
+                       cfg.intermediate_size, cfg.vocab_size, cfg.max_position_embeddings,
+                       cfg.type_vocab_size, cfg.layer_norm_eps)
+
+
+class Model:
+    CACHE_CAPACITY = 1000  # src/lib.rs:249-253
+
+    def __init__(self, handle: int, config: BertConfig, dtype: str, tokenizer=None):
+        self._h = ctypes.c_void_p(handle)
+        self.config = config
+        self.dtype = dtype
+        self.tokenizer = tokenizer
+        self._cache = OrderedDict()
+        self._cache_lock = threading.Lock()
+
+    # ---- construction ---------------------------------------------------
+    @staticmethod
+    def _create(config: BertConfig):
+        L = N.lib()
+        h = ctypes.c_void_p()
+        cs = _cfg_struct(config)
+        N.check(L.ebh_create(ctypes.byref(cs), ctypes.byref(h)))
+        return h
+
+    @staticmethod
+    def _set(h, name: str, arr: np.ndarray):
+        a = np.ascontiguousarray(arr, dtype=np.float32)
+        shape = (ctypes.c_int64 * max(a.ndim, 1))(*a.shape)
+        N.check(N.lib().ebh_set_tensor(h, name.encode(), _ptr(a), shape, a.ndim))
+
+    @classmethod
+    def from_weights(cls, weights: dict, config: BertConfig, dtype: str = "fp32",
+                     tokenizer=None) -> "Model":
+        """Upload HF-named float32 tensors (Linear weights ``[out, in]``) once to HBM."""
+        h = cls._create(config)
+        try:
+            for name, arr in weights.items():
+                cls._set(h, name, arr)
+            N.check(N.lib().ebh_finalize(h, _DTYPES[dtype]))
+        except Exception:
+            N.lib().ebh_destroy(h)
+            raise
+        return cls(h.value, config, dtype, tokenizer)
+
+    @classmethod
+    def from_pretrained_path(cls, path: str, dtype: str = "fp32") -> "Model":
+        """``config.json`` + ``model.safetensors`` (+ ``tokenizer.json`` if present)."""
+        with open(os.path.join(path, "config.json")) as f:
+            c = json.load(f)
+        config = BertConfig(hidden_size=c["hidden_size"],
+                            num_attention_heads=c["num_attention_heads"],
+                            num_hidden_layers=c["num_hidden_layers"],
+                            intermediate_size=c["intermediate_size"],
+                            vocab_size=c["vocab_size"],
+                            max_position_embeddings=c["max_position_embeddings"],
+                            type_vocab_size=c.get("type_vocab_size", 2),
+                            layer_norm_eps=c.get("layer_norm_eps", 1e-12),
+                            hidden_act=c.get("hidden_act", "gelu"),
+                            model_type=c.get("model_type", "bert"))
+        tokenizer = None
+        tok_path = os.path.join(path, "tokenizer.json")
+        if os.path.exists(tok_path):
+            from tokenizers import Tokenizer  # the tokenizer the reference uses (src/lib.rs:314)
+            tokenizer = Tokenizer.from_file(tok_path)
+            if tokenizer.padding is not None:           # BatchLongest (src/lib.rs:317-319)
+                pad = dict(tokenizer.padding)
+                pad.pop("length", None)
+                tokenizer.enable_padding(**{k: v for k, v in pad.items()
+                                            if k in ("direction", "pad_id", "pad_type_id",
+                                                     "pad_token", "pad_to_multiple_of")})
+            if tokenizer.truncation is not None:        # max_length 512 (src/lib.rs:320-322)
+                tr = dict(tokenizer.truncation)
+                tokenizer.enable_truncation(512, stride=tr.get("stride", 0),
+                                            strategy=tr.get("strategy", "longest_first"))
+        h = cls._create(config)
+        try:
+            N.check(N.lib().ebh_load_safetensors(h, os.path.join(path, "model.safetensors").encode()))
+            N.check(N.lib().ebh_finalize(h, _DTYPES[dtype]))
+        except Exception:
+            N.lib().ebh_destroy(h)
+            raise
+        return cls(h.value, config, dtype, tokenizer)
+
+    def close(self):
+        if getattr(self, "_h", None) is not None and self._h.value:
+            N.lib().ebh_destroy(self._h)
+            self._h = ctypes.c_void_p()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    # ---- forward / encode -----------------------------------------------
+    def forward(self, input_ids, attention_mask) -> np.ndarray:
+        """``Model::forward``: f32 ``[B, S]`` ids and mask -> pooled ``[B, H]``."""
+        ids = np.ascontiguousarray(input_ids, dtype=np.float32)
+        mask = np.ascontiguousarray(attention_mask, dtype=np.float32)
+        if ids.ndim != 2 or mask.shape != ids.shape:
+            raise ValueError("input_ids and attention_mask must both be [B, S]")
+        B, S = ids.shape
+        out = np.zeros((B, self.config.hidden_size), np.float32)
+        N.check(N.lib().ebh_forward(self._h, _ptr(ids), _ptr(mask), B, S, _ptr(out)))
+        return out
+
+    def encode_ids(self, ids, mask, normalize: bool = True) -> np.ndarray:
+        """``encode_uncached`` after tokenisation: u32 ids / mask ``[B, S]``."""
+        ids = np.ascontiguousarray(ids, dtype=np.uint32)
+        mask = np.ascontiguousarray(mask, dtype=np.uint32)
+        if ids.ndim != 2 or mask.shape != ids.shape:
+            raise ValueError("ids and mask must both be [B, S]")
+        B, S = ids.shape
+        out = np.zeros((B, self.config.hidden_size), np.float32)
+        N.check(N.lib().ebh_encode(self._h, _ptr(ids), _ptr(mask), B, S, int(bool(normalize)),
+                                   _ptr(out)))
+        return out
+
+    def encode(self, texts, normalize_embeddings: bool = True):
+        """``Model::encode`` (src/lib.rs:479-520): cache lookup, tokenise the misses
+        (special tokens on, BatchLongest padding), run them, cache the results."""
+        if self.tokenizer is None:
+            raise RuntimeError("encode(texts) needs a tokenizer (tokenizer.json); "
+                               "use encode_ids for pre-tokenised input")
+        texts = list(texts)
+        if not texts:
+            return []
+        results = [None] * len(texts)
+        miss_idx, miss_txt = [], []
+        with self._cache_lock:
+            for i, t in enumerate(texts):
+                key = f"{t}||{'true' if normalize_embeddings else 'false'}"
+                if key in self._cache:
+                    self._cache.move_to_end(key)
+                    results[i] = list(self._cache[key])
+                else:
+                    miss_idx.append(i)
+                    miss_txt.append(t)
+        if miss_txt:
+            encs = self.tokenizer.encode_batch(miss_txt, add_special_tokens=True)
+            S = max(len(e.ids) for e in encs)
+            ids = np.zeros((len(encs), S), np.uint32)
+            mask = np.zeros((len(encs), S), np.uint32)
+            for r, e in enumerate(encs):
+                ids[r, :len(e.ids)] = e.ids
+                mask[r, :len(e.attention_mask)] = e.attention_mask
+            emb = self.encode_ids(ids, mask, normalize_embeddings)
+            with self._cache_lock:
+                for r, i in enumerate(miss_idx):
+                    vec = emb[r].tolist()
+                    key = f"{texts[i]}||{'true' if normalize_embeddings else 'false'}"
+                    self._cache[key] = vec
+                    self._cache.move_to_end(key)
+                    while len(self._cache) > self.CACHE_CAPACITY:
+                        self._cache.popitem(last=False)
+                    results[i] = list(vec)
+        return results
+
+    def encode_batch(self, batches, normalize_embeddings: bool = True):
+        """``encode_batch`` (src/lib.rs:440-451): one ``encode`` per sub-batch."""
+        return [self.encode(b, normalize_embeddings) for b in batches]
+
+    # ---- device-resident path (bench / integration) ----------------------
+    def encode_device(self, ids_ptr: int, mask_ptr: int, B: int, S: int, out_ptr: int,
+                      normalize: bool = True, stream: int | None = None):
+        """Enqueue a forward over device buffers (int32 ids / mask, f32 out)."""
+        N.check(N.lib().ebh_encode_device(self._h, ctypes.c_void_p(ids_ptr),
+                                          ctypes.c_void_p(mask_ptr), B, S, int(bool(normalize)),
+                                          ctypes.c_void_p(out_ptr),
+                                          ctypes.c_void_p(stream) if stream else None))
+
+    def synchronize(self):
+        N.check(N.lib().ebh_synchronize(self._h))
+
+    def last_tokens(self, B: int):
+        n = ctypes.c_int32()
+        N.check(N.lib().ebh_last_tokens(self._h, None, None, 0, None, 0, ctypes.byref(n)))
+        tok_ids = np.zeros(max(n.value, 1), np.int32)
+        tok_pos = np.zeros(max(n.value, 1), np.int32)
+        cu = np.zeros(B + 1, np.int32)
+        N.check(N.lib().ebh_last_tokens(self._h, _ptr(tok_ids), _ptr(tok_pos), tok_ids.size,
+                                        _ptr(cu), cu.size, ctypes.byref(n)))
+        return tok_ids[:n.value], tok_pos[:n.value], cu
+
+    def profile_enable(self, kernel: str):
+        N.check(N.lib().ebh_profile_enable(self._h, N.PROF[kernel]))
+
+    def profile_read(self):
+        launches, ms = ctypes.c_int64(), ctypes.c_double()
+        N.check(N.lib().ebh_profile_read(self._h, ctypes.byref(launches), ctypes.byref(ms)))
+        return launches.value, ms.value
+
+
+def cosine_similarity(a, b) -> float:
+    """``cosine_similarity`` (src/lib.rs:756-789): dot / (|a||b| + 1e-8)."""
+    a = np.asarray(a, np.float32)
+    b = np.asarray(b, np.float32)
+    n = min(a.size, b.size)
+    dot = np.float32(np.dot(a[:n], b[:n]))
+    return float(dot / (np.float32(np.linalg.norm(a)) * np.float32(np.linalg.norm(b)) + np.float32(1e-8)))

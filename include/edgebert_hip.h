@@ -1,0 +1,153 @@
+/*
+ * edgebert_hip.h -- C ABI of the MI355X (gfx950) BERT encoder forward.
+ *
+ * Drop-in for the body of EdgeBERT's `Model::forward` plus the normalisation
+ * tail of `encode_uncached` (/root/reference/src/lib.rs:588-666).  The host
+ * tokenizer and the public `encode` / cache logic stay with the caller; a Rust
+ * `hip` backend binds these symbols with `extern "C"` (the binding is shown in
+ * INTEGRATION.md).
+ *
+ * Conventions
+ *  - Every function returns EBH_OK (0) on success or a negative EBH_ERR_*
+ *    code; the message of the calling thread's last failure is returned by
+ *    ebh_last_error() (thread-local, valid until the next failing call).
+ *  - The caller owns every host buffer; the library owns the device weights
+ *    and a workspace that grows on demand.  Calls on one model are
+ *    serialised internally, so a model may be shared by many host threads
+ *    (as `encode(&self)` is under rayon, src/lib.rs:440-451).
+ *  - Linear weights are given in the HF [out, in] layout, exactly as stored
+ *    in model.safetensors; the library re-lays them out for the GPU.
+ */
+#ifndef EDGEBERT_HIP_H
+#define EDGEBERT_HIP_H
+
+#include <stdint.h>
+
+#ifndef EBH_API
+#define EBH_API __attribute__((visibility("default")))
+#endif
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define EBH_OK 0
+#define EBH_ERR_INVALID_ARG (-1) /* null pointer, negative size, bad config     */
+#define EBH_ERR_NOT_FOUND (-2)   /* unknown / missing tensor name               */
+#define EBH_ERR_SHAPE (-3)       /* tensor rank or shape does not match config  */
+#define EBH_ERR_STATE (-4)       /* e.g. forward before finalize                */
+#define EBH_ERR_HIP (-5)         /* HIP runtime failure                         */
+#define EBH_ERR_RANGE (-6)       /* token id >= vocab, S > max positions, ...   */
+
+#define EBH_DTYPE_F32 0  /* fp32 GEMMs (parity path)                          */
+#define EBH_DTYPE_BF16 1 /* bf16 GEMM inputs, fp32 accumulate; LN/softmax fp32 */
+
+typedef struct ebh_model ebh_model;
+
+/* Mirrors the reference `Config` (src/lib.rs:95-106).  hidden_act is not a
+ * field: the reference ignores it and always applies the tanh GELU
+ * (src/lib.rs:958-978). type_vocab_size is the row count of
+ * embeddings.token_type_embeddings.weight (the reference reads it from the
+ * tensor shape). */
+typedef struct ebh_config {
+    int32_t hidden_size;
+    int32_t num_attention_heads;
+    int32_t num_hidden_layers;
+    int32_t intermediate_size;
+    int32_t vocab_size;
+    int32_t max_position_embeddings;
+    int32_t type_vocab_size;
+    float layer_norm_eps;
+} ebh_config;
+
+/* Message of this thread's most recent failure ("" if none). */
+EBH_API const char* ebh_last_error(void);
+
+/* Model::from_weights, step 1 (src/lib.rs:155-159): validate the config and
+ * create an empty model (no HIP call is made before ebh_finalize).
+ * hidden_size must be a multiple of num_attention_heads with head_dim 32 or
+ * 64, hidden_size <= 2048, and hidden_size / intermediate_size multiples of 8. */
+EBH_API int ebh_create(const ebh_config* cfg, ebh_model** out);
+
+/* ModelWeights::get_array1/2 + from_weights field mapping
+ * (src/weights.rs:47-69, src/lib.rs:161-238): hand over one tensor by its HF
+ * name.  Data is copied; shape must match the config.  Unknown names fail
+ * with EBH_ERR_NOT_FOUND, a wrong rank/shape with EBH_ERR_SHAPE
+ * ("Expected 1D tensor ..." as in src/weights.rs:53-57). */
+EBH_API int ebh_set_tensor(ebh_model* m, const char* name, const float* data, const int64_t* shape,
+                   int32_t ndim);
+
+/* Load every tensor from a model.safetensors file (src/weights.rs:15-45).
+ * F32 tensors are read as-is; F16 and BF16 are widened to f32.  Tensors the
+ * encoder does not use (pooler.*, classifier.*) are skipped. */
+EBH_API int ebh_load_safetensors(ebh_model* m, const char* path);
+
+/* End of from_weights: check that every tensor is present (missing ->
+ * EBH_ERR_NOT_FOUND "Tensor <name> not found"), bind the model to the
+ * current HIP device, upload all weights once into
+ * one device-resident HBM block (QKV concatenated to [3H, H]) and, for
+ * EBH_DTYPE_BF16, keep bf16 copies of the GEMM weights. */
+EBH_API int ebh_finalize(ebh_model* m, int32_t dtype);
+
+EBH_API void ebh_destroy(ebh_model* m);
+
+/* Model::forward (src/lib.rs:621-666) on host buffers:
+ * input_ids / attention_mask are the reference's f32 [B, S] row-major arrays
+ * (src/lib.rs:588-601); out is [B, hidden_size] mean-pooled, NOT normalised.
+ * ids are converted like `token_id as usize` (truncation, negatives -> 0) and
+ * must be < vocab_size (the reference panics otherwise: EBH_ERR_RANGE); mask
+ * values must be 0 or 1.  S must be <= max_position_embeddings.  B == 0 is a
+ * no-op; S == 0 yields zero rows; an all-zero mask row yields NaN, as the
+ * reference's -inf softmax does.  Blocking. */
+EBH_API int ebh_forward(ebh_model* m, const float* input_ids, const float* attention_mask, int32_t B,
+                int32_t S, float* out);
+
+/* encode_uncached after tokenisation (src/lib.rs:573-619): u32 ids and mask
+ * from the tokenizer's encodings, zero-padded to [B, S]; out [B, hidden_size]
+ * L2-normalised (x / max(||x||, 1e-12)) when normalize != 0.  Blocking. */
+EBH_API int ebh_encode(ebh_model* m, const uint32_t* ids, const uint32_t* mask, int32_t B, int32_t S,
+               int32_t normalize, float* out);
+
+/* Device-pointer variant of ebh_encode for callers that keep ids / mask /
+ * output in HBM: int32 ids and 0/1 mask [B, S], out [B, hidden_size], all
+ * device pointers; enqueued on `stream` (a hipStream_t, NULL = the model's own
+ * stream) and returns without waiting.  Ids are range-checked on the device:
+ * an id >= vocab_size reads row 0 and is reported by the next
+ * ebh_synchronize().  Successive calls are ordered even across streams. */
+EBH_API int ebh_encode_device(ebh_model* m, const int32_t* ids, const int32_t* mask, int32_t B,
+                      int32_t S, int32_t normalize, float* out, void* stream);
+
+/* Wait for the model's outstanding work; EBH_ERR_RANGE if a device-side id
+ * check failed since the previous ebh_synchronize / blocking call. */
+EBH_API int ebh_synchronize(ebh_model* m);
+
+/* The packed token stream the last forward consumed: n_tokens (mask == 1
+ * tokens) ids and original positions, and cu_seqlens [B+1].  Any output
+ * pointer may be NULL; capacities are in elements.  Used to check that the
+ * ids reaching the GPU are bit-identical to the caller's.  Blocking. */
+EBH_API int ebh_last_tokens(ebh_model* m, int32_t* tok_ids, int32_t* tok_pos, int64_t tok_capacity,
+                    int32_t* cu_seqlens, int64_t cu_capacity, int32_t* n_tokens);
+
+/* Hidden size / dtype of a finalized model (for bindings that size outputs). */
+EBH_API int ebh_model_info(const ebh_model* m, ebh_config* cfg_out, int32_t* dtype_out);
+
+/* Time one kernel family with HIP events during forwards, on the stream the
+ * kernels are launched on.  kernel: one of EBH_PROF_* (EBH_PROF_NONE = off).
+ * ebh_profile_read returns the accumulated launch count and total ms since the
+ * last ebh_profile_enable, after waiting for the model's work. */
+#define EBH_PROF_NONE 0
+#define EBH_PROF_GEMM_QKV 1
+#define EBH_PROF_ATTENTION 2
+#define EBH_PROF_GEMM_OUT 3
+#define EBH_PROF_GEMM_FFN_UP 4
+#define EBH_PROF_GEMM_FFN_DOWN 5
+#define EBH_PROF_LAYERNORM 6
+#define EBH_PROF_EMBED 7
+#define EBH_PROF_POOL 8
+EBH_API int ebh_profile_enable(ebh_model* m, int32_t kernel);
+EBH_API int ebh_profile_read(ebh_model* m, int64_t* launches, double* total_ms);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* EDGEBERT_HIP_H */

@@ -1,0 +1,77 @@
+/*
+ * edgebert_hip_ops.h -- op-level entry points of the gfx950 encoder kernels.
+ *
+ * Each call enqueues one kernel (family) on `stream` (a hipStream_t; NULL =
+ * the null stream) over caller-owned DEVICE buffers and returns without
+ * waiting.  They exist so that every kernel can be checked and timed alone
+ * against the reference op it replaces; the model-level API in
+ * edgebert_hip.h chains the same kernels.  Return codes as in
+ * edgebert_hip.h (arguments are validated on the host before any launch).
+ */
+#ifndef EDGEBERT_HIP_OPS_H
+#define EDGEBERT_HIP_OPS_H
+
+#include <stdint.h>
+
+#ifndef EBH_API
+#define EBH_API __attribute__((visibility("default")))
+#endif
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define EBH_EPI_BIAS 0       /* C = A.W^T + b                       */
+#define EBH_EPI_BIAS_GELU 1  /* C = gelu_tanh(A.W^T + b)             */
+#define EBH_EPI_BIAS_RESID 2 /* C = (A.W^T + b) + R                  */
+
+/* matmul_3d_2d + bias (+ gelu / + residual) (src/lib.rs:795-849, 691-698,
+ * 732-733, 741-747, 673, 678, 958-978), batch folded into M:
+ * A [M, K] fp32 (row stride lda), W [N, K] HF layout (row stride ldw), fp32
+ * when w_dtype == EBH_DTYPE_F32 or bf16 bits (uint16) when EBH_DTYPE_BF16 (A
+ * is then rounded to bf16 on load; accumulation is fp32).  C [M, N] (ldc);
+ * residual [M, N] (ldr) only for EBH_EPI_BIAS_RESID.  K and the strides must
+ * be multiples of 4 (fp32) / 8 (bf16). */
+EBH_API int ebh_op_gemm(const float* A, int64_t lda, const void* W, int64_t ldw, int32_t w_dtype,
+                const float* bias, const float* residual, int64_t ldr, float* C, int64_t ldc,
+                int32_t M, int32_t N, int32_t K, int32_t epilogue, void* stream);
+
+/* Masked multi-head attention (src/lib.rs:700-730 with 851-956) over packed
+ * sequences: qkv [T, 3*hidden] rows (q | k | v), sequence b = rows
+ * cu_seqlens[b] .. cu_seqlens[b+1]-1 (every row a real token, lengths <=
+ * max_len); ctx [T, hidden].  head_dim = hidden / num_heads must be 32 or 64;
+ * scale is 1/sqrt(head_dim) as the reference computes it (src/lib.rs:196-197). */
+EBH_API int ebh_op_attention(const float* qkv, const int32_t* cu_seqlens, int32_t B, int32_t max_len,
+                     int32_t hidden, int32_t num_heads, float* ctx, void* stream);
+
+/* apply_layer_norm_3d (src/lib.rs:980-991) over rows x [rows, H] -> y (may alias). */
+EBH_API int ebh_op_layer_norm(const float* x, const float* gamma, const float* beta, int32_t rows,
+                      int32_t H, float eps, float* y, void* stream);
+
+/* mean_pool (src/lib.rs:993-1010) over packed sequences (+ the normalise tail,
+ * src/lib.rs:605-612, when normalize != 0); S is the padded length the caller
+ * had (S > 0 and an empty sequence gives NaN, as in the reference). */
+EBH_API int ebh_op_pool(const float* x, const int32_t* cu_seqlens, int32_t B, int32_t H, int32_t S,
+                int32_t normalize, float* out, void* stream);
+
+/* Token packing: ids / mask [B, S] -> cu_seqlens [B+1], n_tokens [1],
+ * tok_id / tok_pos [B*S]; counts [B] is scratch; err [1] is cleared. */
+EBH_API int ebh_op_pack(const int32_t* ids, const int32_t* mask, int32_t B, int32_t S,
+                int32_t* counts, int32_t* cu_seqlens, int32_t* n_tokens, int32_t* tok_id,
+                int32_t* tok_pos, int32_t* err, void* stream);
+
+/* Embedding rows word[tok_id] + pos[tok_pos] + type0, then LayerNorm
+ * (src/lib.rs:628-661), for the first *n_tokens (device) of T_max tokens;
+ * ids outside [0, V) read row 0 and set *err |= 1. */
+EBH_API int ebh_op_embed_ln(const int32_t* tok_id, const int32_t* tok_pos, const int32_t* n_tokens,
+                    int32_t T_max, const float* word, const float* pos, const float* type0,
+                    const float* gamma, const float* beta, int32_t V, int32_t H, float eps,
+                    float* x, int32_t* err, void* stream);
+
+/* fp32 -> bf16 bits, round to nearest even (weight conversion). */
+EBH_API int ebh_op_f32_to_bf16(const float* x, uint16_t* y, int64_t n, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* EDGEBERT_HIP_OPS_H */

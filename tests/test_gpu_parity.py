@@ -1,0 +1,117 @@
+"""Parity of the HIP path (through the C ABI) with the CPU oracle.
+
+Bars: token ids bit-exact; fp32 max-abs embedding
+difference <= 1e-4 and cosine >= 0.99999 per sequence against the oracle's
+run of that sequence alone, unpadded; bf16 GEMMs cosine >= 0.999.
+"""
+import numpy as np
+import pytest
+
+from conftest import cosine_rows
+
+pytestmark = pytest.mark.gpu
+
+FP32_MAX_ABS = 1e-4
+FP32_MIN_COS = 0.99999
+BF16_MIN_COS = 0.999
+
+
+@pytest.fixture(scope="module")
+def eb():
+    import edgebert_amd
+    edgebert_amd.lib()
+    return edgebert_amd
+
+
+@pytest.fixture(scope="module")
+def oracle_mod():
+    import oracle
+    return oracle
+
+
+_MODELS = {}
+
+
+def gpu_model(eb, cfg, weights, dtype="fp32"):
+    key = (cfg, dtype)
+    if key not in _MODELS:
+        _MODELS[key] = eb.Model.from_weights(weights, cfg, dtype)
+    return _MODELS[key]
+
+
+def _report(name, got, want):
+    err = float(np.abs(got - want).max())
+    cos = float(cosine_rows(got, want).min())
+    print(f"{name}: max_abs={err:.3e} min_cos={cos:.9f}", flush=True)
+    return err, cos
+
+
+@pytest.mark.parametrize("cname", ["c1", "c2", "c4"])
+def test_encode_matches_unpadded_oracle(eb, oracle_mod, weights_for, cname):
+    spec = eb.CONFIGS[cname]
+    w = weights_for(spec.model)
+    ids, mask, lengths = eb.make_inputs(spec)
+    m = gpu_model(eb, spec.model, w)
+    got = m.encode_ids(ids, mask, normalize=True)
+    want = oracle_mod.OracleModel(spec.model, w).encode_unpadded(ids, mask, normalize=True)
+    err, cos = _report(f"{cname} encode vs unpadded oracle", got, want)
+    assert err <= FP32_MAX_ABS and cos >= FP32_MIN_COS
+    tok, pos, cu = m.last_tokens(spec.batch)
+    assert np.array_equal(tok, ids[mask != 0]), "token ids reaching the GPU differ"
+    assert np.array_equal(pos, np.nonzero(mask)[1].astype(np.int32))
+    assert np.array_equal(cu, np.concatenate([[0], np.cumsum(lengths)]).astype(np.int32))
+
+
+@pytest.mark.parametrize("cname", ["c1", "c2"])
+def test_forward_matches_padded_oracle(eb, oracle_mod, weights_for, cname):
+    """Model::forward on the reference's f32 arrays vs the oracle's padded run."""
+    spec = eb.CONFIGS[cname]
+    w = weights_for(spec.model)
+    ids, mask, _ = eb.make_inputs(spec)
+    m = gpu_model(eb, spec.model, w)
+    got = m.forward(ids.astype(np.float32), mask.astype(np.float32))
+    want = oracle_mod.OracleModel(spec.model, w).forward(ids.astype(np.float32),
+                                                         mask.astype(np.float32))
+    err, cos = _report(f"{cname} forward vs padded oracle", got, want)
+    assert err <= FP32_MAX_ABS and cos >= FP32_MIN_COS
+
+
+def test_c3_subsample_and_properties(eb, oracle_mod, weights_for):
+    """Headline shape (256 x 128): 16 sequences against the oracle, and
+    size-independent properties over the whole batch."""
+    spec = eb.CONFIGS["c3"]
+    w = weights_for(spec.model)
+    ids, mask, _ = eb.make_inputs(spec)
+    m = gpu_model(eb, spec.model, w)
+    got = m.encode_ids(ids, mask, normalize=True)
+    assert np.isfinite(got).all()
+    np.testing.assert_allclose(np.linalg.norm(got.astype(np.float64), axis=1), 1.0, atol=1e-5)
+    sel = np.arange(0, spec.batch, spec.batch // 16)
+    want = oracle_mod.OracleModel(spec.model, w).encode(ids[sel], mask[sel], normalize=True)
+    err, cos = _report("c3 subsample", got[sel], want)
+    assert err <= FP32_MAX_ABS and cos >= FP32_MIN_COS
+    # batch-permutation equivariance: each row is computed independently of its slot
+    perm = np.random.default_rng(0).permutation(spec.batch)
+    got_p = m.encode_ids(ids[perm], mask[perm], normalize=True)
+    assert np.array_equal(got_p, got[perm])
+    # duplicated sentences give identical vectors (self-cosine 1, src/lib.rs:1255-1258)
+    dup = np.repeat(ids[:4], 2, axis=0)
+    got_d = m.encode_ids(dup, np.ones_like(dup), normalize=True)
+    assert np.array_equal(got_d[0::2], got_d[1::2])
+
+
+def test_bf16_bert_base(eb, oracle_mod, weights_for):
+    """c5 shape (BERT-base, head_dim 64) with bf16 GEMMs on a 24-sequence sample."""
+    spec = eb.CONFIGS["c5"]
+    w = weights_for(spec.model)
+    ids, mask, _ = eb.make_inputs(spec)
+    ids, mask = ids[:24], mask[:24]
+    want = oracle_mod.OracleModel(spec.model, w).encode(ids, mask, normalize=True)
+    m16 = gpu_model(eb, spec.model, w, "bf16")
+    got16 = m16.encode_ids(ids, mask, normalize=True)
+    _, cos16 = _report("c5 bf16 vs fp32 oracle", got16, want)
+    assert cos16 >= BF16_MIN_COS
+    m32 = gpu_model(eb, spec.model, w, "fp32")
+    got32 = m32.encode_ids(ids, mask, normalize=True)
+    err, cos = _report("c5-shape fp32 vs oracle", got32, want)
+    assert err <= FP32_MAX_ABS and cos >= FP32_MIN_COS
