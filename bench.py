@@ -1,20 +1,26 @@
 """Throughput of the gfx950 BERT encoder forward (BASELINE.json metric).
 
 One step = one ``ebh_encode_device`` forward of the whole batch (embeddings ->
-6 layers -> mean pool -> L2 normalise) over ids / mask already resident in
+L layers -> mean pool -> L2 normalise) over ids / mask already resident in
 HBM, ending with the stream synchronised.  Default workload: c3, MiniLM-L6
 shape, batch 256 x seq 128, fp32, seeded synthetic ids, random-init weights.
 
-Prints one JSON line.  ``roofline`` is measured live for the dominant kernel
-(the FFN-up GEMM) with HIP events on the stream its launches go to;
-``cpu_baseline`` times the repo's C restatement of the reference CPU path
-(``oracle/``) on a bounded sample of the same workload on this host.
+Prints one JSON line.  ``roofline`` is measured live for one kernel family
+(default: the FFN-up GEMM, the largest single launch) with HIP events on the
+stream its launches go to; its ``traffic`` (HBM bytes per launch) is read from
+the committed rocprofv3 counter summary for the same workload and kernel, when
+there is one.  ``cpu_baseline`` times the repo's C restatement of the
+reference CPU path (``oracle/``) on a bounded sample of the same workload on
+this host.  ``host_api`` is the rate of the blocking host-buffer entry point
+(``ebh_encode``: ids / mask copied in over PCIe, vectors copied back); it is
+reported beside ``value``, never as it.
 """
 from __future__ import annotations
 
 import argparse
 import json
 import os
+import re
 import sys
 import time
 
@@ -23,14 +29,40 @@ import numpy as np
 ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
-PEAK = {"fp32": (157.3, "TFLOP/s"), "bf16": (2500.0, "TFLOP/s")}   # MI355X dense MFMA peaks
+# MI355X published dense peaks: fp32 matrix 157.3 TFLOP/s, bf16 2.5 PFLOP/s; HBM3E 8 TB/s.
+PEAK_TFLOPS = {"fp32": 157.3, "bf16": 2500.0}
 HBM_PEAK_GBS = 8000.0
+KERNELS = ("gemm_qkv", "attention", "gemm_out", "gemm_ffn_up", "gemm_ffn_down", "layernorm",
+           "embed", "pool")
 
 
-def gemm_flops(cfg, tokens: int, which: str) -> float:
+def kernel_work(cfg, lengths, B: int, which: str):
+    """Algorithmic work of ONE launch of a kernel family: (amount, bound, unit).
+
+    GEMMs: 2*T*N*K FLOPs over the T valid tokens.  Attention: 4*H*sum(l^2)
+    FLOPs (q.k^T and p.v at 2 FLOP per MAC).  Row kernels: the HBM bytes the
+    op must move at minimum (each operand read once, each result written once).
+    """
     H, I = cfg.hidden_size, cfg.intermediate_size
-    return {"gemm_qkv": 2.0 * tokens * H * 3 * H, "gemm_out": 2.0 * tokens * H * H,
-            "gemm_ffn_up": 2.0 * tokens * H * I, "gemm_ffn_down": 2.0 * tokens * I * H}[which]
+    lengths = np.asarray(lengths, np.float64)
+    T = float(lengths.sum())
+    if which == "gemm_qkv":
+        return 2.0 * T * H * 3 * H, "mfma", "flop"
+    if which == "gemm_out":
+        return 2.0 * T * H * H, "mfma", "flop"
+    if which == "gemm_ffn_up":
+        return 2.0 * T * H * I, "mfma", "flop"
+    if which == "gemm_ffn_down":
+        return 2.0 * T * I * H, "mfma", "flop"
+    if which == "attention":
+        return 4.0 * H * float((lengths ** 2).sum()), "mfma", "flop"
+    if which == "layernorm":          # read the GEMM output row, write the normalised row
+        return 2.0 * T * H * 4 + 2 * H * 4, "hbm", "byte"
+    if which == "embed":              # token id + position, word/position rows, written row
+        return T * (8 + 3 * H * 4) + 3 * H * 4, "hbm", "byte"
+    if which == "pool":               # every token row once, one vector per sequence
+        return T * H * 4 + B * H * 4 + (B + 1) * 4, "hbm", "byte"
+    raise KeyError(which)
 
 
 def forward_flops(cfg, lengths) -> float:
@@ -38,6 +70,21 @@ def forward_flops(cfg, lengths) -> float:
     H, I, L = cfg.hidden_size, cfg.intermediate_size, cfg.num_hidden_layers
     lengths = np.asarray(lengths, np.float64)
     return float(L * (2 * lengths * (4 * H * H + 2 * H * I) + 4 * lengths ** 2 * H).sum())
+
+
+def measured_traffic(config: str, kernel: str, dtype: str):
+    """HBM bytes per launch from the committed counter summary
+    (profiles/hbm_traffic_<config>.md, lines ``traffic[<kernel>][<dtype>] = <bytes>``)."""
+    path = os.path.join(ROOT, "profiles", f"hbm_traffic_{config}.md")
+    if not os.path.exists(path):
+        return None
+    pat = re.compile(r"^traffic\[(\w+)\]\[(\w+)\]\s*=\s*(\d+)")
+    with open(path) as f:
+        for line in f:
+            m = pat.match(line.strip())
+            if m and m.group(1) == kernel and m.group(2) == dtype:
+                return int(m.group(3))
+    return None
 
 
 def cpu_baseline(spec, weights, ids, mask, budget_s: float):
@@ -60,7 +107,7 @@ def cpu_baseline(spec, weights, ids, mask, budget_s: float):
             "cores": oracle.get_num_threads(), "kind": "port",
             "sample": f"{done} sequences of the {spec.name} workload (seq {spec.seq_len}) in "
                       f"chunks of {chunk}, {el:.1f} s, oracle/liboracle.so on "
-                      f"{oracle.get_num_threads()} OpenMP threads"}
+                      f"{oracle.get_num_threads()} OpenMP threads of {os.cpu_count()} host CPUs"}
 
 
 def main():
@@ -70,9 +117,14 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--config", default="c3", choices=["c1", "c2", "c3", "c4", "c5"])
     ap.add_argument("--dtype", default=None, help="fp32 | bf16 (default: the config's)")
-    ap.add_argument("--profile-kernel", default="gemm_ffn_up")
+    ap.add_argument("--profile-kernel", default="gemm_ffn_up", choices=KERNELS)
     ap.add_argument("--cpu-budget", type=float, default=12.0,
                     help="seconds of CPU baseline work (0 disables)")
+    ap.add_argument("--host-api-steps", type=int, default=5,
+                    help="blocking host-buffer forwards timed for host_api (0 disables)")
+    ap.add_argument("--copy-probe-mb", type=int, default=0,
+                    help="after the timed region, run 3 plain device copies of this many MiB "
+                         "(the calibration dispatch for rocprofv3 FETCH_SIZE / WRITE_SIZE)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU only; --gpus {args.gpus} is not supported "
@@ -126,9 +178,11 @@ def main():
     value = B * args.steps / wall
     tokens = int(mask.sum())
     avg_kernel_ms = prof_ms / max(launches, 1)
-    flops = gemm_flops(cfg, tokens, args.profile_kernel)
-    achieved = flops / (avg_kernel_ms * 1e-3) / 1e12
-    peak, punit = PEAK[dtype]
+    work, bound, wunit = kernel_work(cfg, lengths, B, args.profile_kernel)
+    if bound == "mfma":
+        achieved, peak, punit = work / (avg_kernel_ms * 1e-3) / 1e12, PEAK_TFLOPS[dtype], "TFLOP/s"
+    else:
+        achieved, peak, punit = work / (avg_kernel_ms * 1e-3) / 1e9, HBM_PEAK_GBS, "GB/s"
     fwd_flops = forward_flops(cfg, lengths)
 
     result = {
@@ -152,11 +206,29 @@ def main():
                    "global_batch": B, "seq_len": S, "valid_tokens": tokens,
                    "parallelism": "single GPU"},
         "forward_tflops": round(fwd_flops / (ms_per_step * 1e-3) / 1e12, 2),
-        "roofline": {"kernel": args.profile_kernel, "bound": "mfma", "achieved": round(achieved, 3),
+        "roofline": {"kernel": args.profile_kernel, "bound": bound, "achieved": round(achieved, 3),
                      "peak": peak, "unit": punit, "frac": round(achieved / peak, 4),
-                     "traffic": None, "avg_launch_ms": round(avg_kernel_ms, 5),
-                     "launches": launches},
+                     "traffic": measured_traffic(args.config, args.profile_kernel, dtype),
+                     "work_per_launch": work, "work_unit": wunit,
+                     "avg_launch_ms": round(avg_kernel_ms, 5), "launches": launches},
     }
+    if args.host_api_steps > 0:
+        model.encode_ids(ids, mask, normalize=True)           # warm the host staging buffers
+        t0 = time.perf_counter()
+        for _ in range(args.host_api_steps):
+            model.encode_ids(ids, mask, normalize=True)
+        el = time.perf_counter() - t0
+        result["host_api"] = {"value": round(B * args.host_api_steps / el, 2),
+                              "unit": "sentences/s",
+                              "note": "ebh_encode on host buffers: validation + H2D + forward + D2H"}
+    if args.copy_probe_mb > 0:
+        n = args.copy_probe_mb * (1 << 20) // 4
+        src = torch.ones(n, dtype=torch.float32, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        result["copy_probe_bytes"] = n * 4
     if args.cpu_budget > 0:
         result["cpu_baseline"] = cpu_baseline(spec, weights, ids, mask, args.cpu_budget)
     print(json.dumps(result), flush=True)

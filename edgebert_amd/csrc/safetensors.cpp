@@ -213,9 +213,19 @@ extern "C" int ebh_load_safetensors(ebh_model* m, const char* path) {
         std::vector<int64_t> shape;
         uint64_t count = 1;
         for (auto& d : shp.arr) {
+            // Dimensions are non-negative integers; 2^40 bounds the element
+            // count of any tensor this model could hold.
+            if (d.kind != JVal::NUM || !(d.num >= 0.0) || d.num != (double)(int64_t)d.num ||
+                d.num > (double)(1ull << 40))
+                return fail(EBH_ERR_SHAPE, ("safetensors: bad shape for " + name).c_str());
             shape.push_back((int64_t)d.num);
             count *= (uint64_t)d.num;
+            if (count > (1ull << 40))
+                return fail(EBH_ERR_SHAPE, ("safetensors: bad shape for " + name).c_str());
         }
+        for (auto& o : offs.arr)
+            if (o.kind != JVal::NUM || !(o.num >= 0.0) || o.num > 9.0e15)
+                return fail(EBH_ERR_SHAPE, ("safetensors: bad data_offsets for " + name).c_str());
         const uint64_t b0 = (uint64_t)offs.arr[0].num, b1 = (uint64_t)offs.arr[1].num;
         const int esz = dt == "F32" ? 4 : (dt == "F16" || dt == "BF16") ? 2 : 0;
         if (!esz)

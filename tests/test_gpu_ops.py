@@ -1,0 +1,446 @@
+"""Each HIP kernel alone, through the op-level C ABI (include/edgebert_hip_ops.h),
+against a float64 reference of the reference op it replaces; then the
+model-level edge cases of the forward (empty batch, S = 0, all-masked row,
+masks with holes, ids out of range, concurrent callers, workspace growth,
+safetensors loading).  Device memory comes from torch; every call is
+enqueued on torch's current stream."""
+import ctypes
+import json
+import os
+import threading
+
+import numpy as np
+import pytest
+
+from conftest import cosine_rows
+
+pytestmark = pytest.mark.gpu
+
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "encoder_golden.npz")
+
+
+@pytest.fixture(scope="module")
+def env():
+    import torch
+    import edgebert_amd as eb
+    from edgebert_amd import _native as N
+    assert torch.cuda.is_available(), "gpu tests need a GPU"
+    return torch, eb, N, eb.lib()
+
+
+def vp(t):
+    """Device address of a tensor the caller keeps alive until the work is done
+    (a temporary would return its block to torch's allocator at once, and the
+    next allocation could take it over before the kernel reads it)."""
+    return ctypes.c_void_p(t.data_ptr())
+
+
+def stream(torch):
+    return ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+
+def dev(torch, a):
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+# ---------------------------------------------------------------------------
+# GEMM family (matmul_3d_2d + bias / GELU / residual)
+# ---------------------------------------------------------------------------
+def gelu64(x):
+    return 0.5 * x * (1 + np.tanh(0.7978845608 * (x + 0.044715 * x ** 3)))
+
+
+GEMM_SHAPES = [(1, 8, 4), (7, 40, 12), (130, 1152, 384), (257, 384, 1536), (64, 96, 64),
+               (300, 1536, 384), (33, 768, 3072)]
+
+
+@pytest.mark.parametrize("M,N,K", GEMM_SHAPES)
+@pytest.mark.parametrize("epi", [0, 1, 2])
+def test_gemm_f32(env, M, N, K, epi):
+    torch, eb, Nn, L = env
+    rng = np.random.default_rng(M * 7 + N + K + epi)
+    lda = K + 4                                   # a row stride above K
+    A = rng.standard_normal((M, lda)).astype(np.float32)
+    W = (0.05 * rng.standard_normal((N, K))).astype(np.float32)
+    bias = rng.standard_normal(N).astype(np.float32)
+    R = rng.standard_normal((M, N)).astype(np.float32)
+    dA, dW, db, dR = dev(torch, A), dev(torch, W), dev(torch, bias), dev(torch, R)
+    dC = torch.full((M, N), float("nan"), device="cuda")
+    Nn.check(L.ebh_op_gemm(vp(dA), lda, vp(dW), K, Nn.EBH_DTYPE_F32, vp(db),
+                           vp(dR) if epi == 2 else None, N, vp(dC), N, M, N, K, epi, stream(torch)))
+    torch.cuda.synchronize()
+    want = A[:, :K].astype(np.float64) @ W.T.astype(np.float64) + bias
+    if epi == 1:
+        want = gelu64(want)
+    if epi == 2:
+        want = want + R
+    got = dC.cpu().numpy()
+    tol = 2e-6 * np.sqrt(K) * (np.abs(A[:, :K]).max() * np.abs(W).max() * np.sqrt(K)) + 1e-5
+    np.testing.assert_allclose(got, want, rtol=0, atol=tol)
+
+
+def _bf16_round(x):
+    import torch
+    return torch.from_numpy(np.ascontiguousarray(x, np.float32)).to(torch.bfloat16).float().numpy()
+
+
+@pytest.mark.parametrize("M,N,K", [(5, 16, 8), (130, 2304, 768), (257, 768, 3072), (64, 1536, 384)])
+@pytest.mark.parametrize("epi", [0, 1, 2])
+def test_gemm_bf16(env, M, N, K, epi):
+    """bf16 inputs (A rounded on load, W pre-converted), fp32 accumulate: equal to
+    the float64 product of the bf16-rounded operands up to fp32 summation."""
+    torch, eb, Nn, L = env
+    rng = np.random.default_rng(M + N + K + epi)
+    A = rng.standard_normal((M, K)).astype(np.float32)
+    W = (0.05 * rng.standard_normal((N, K))).astype(np.float32)
+    bias = rng.standard_normal(N).astype(np.float32)
+    R = rng.standard_normal((M, N)).astype(np.float32)
+    dA, dW32, db, dR = dev(torch, A), dev(torch, W), dev(torch, bias), dev(torch, R)
+    dW16 = torch.empty((N, K), dtype=torch.int16, device="cuda")
+    Nn.check(L.ebh_op_f32_to_bf16(vp(dW32), vp(dW16), N * K, stream(torch)))
+    dC = torch.empty((M, N), device="cuda")
+    Nn.check(L.ebh_op_gemm(vp(dA), K, vp(dW16), K, Nn.EBH_DTYPE_BF16, vp(db),
+                           vp(dR) if epi == 2 else None, N, vp(dC), N, M, N, K, epi, stream(torch)))
+    torch.cuda.synchronize()
+    want = _bf16_round(A).astype(np.float64) @ _bf16_round(W).T.astype(np.float64) + bias
+    if epi == 1:
+        want = gelu64(want)
+    if epi == 2:
+        want = want + R
+    np.testing.assert_allclose(dC.cpu().numpy(), want, rtol=0, atol=2e-5 * np.sqrt(K))
+
+
+def test_f32_to_bf16_round_to_nearest_even(env):
+    torch, eb, Nn, L = env
+    rng = np.random.default_rng(3)
+    x = np.concatenate([rng.standard_normal(10000).astype(np.float32) * 100,
+                        np.array([0.0, -0.0, np.inf, -np.inf, 1e-40, -1e-39, 3.4e38, 1.0 + 2 ** -8,
+                                  1.0 + 3 * 2 ** -8, np.nan], np.float32)])
+    dx = dev(torch, x)
+    dy = torch.empty(x.size, dtype=torch.int16, device="cuda")
+    Nn.check(L.ebh_op_f32_to_bf16(vp(dx), vp(dy), x.size, stream(torch)))
+    torch.cuda.synchronize()
+    got = dy.cpu().numpy().view(np.uint16)
+    want = torch.from_numpy(x).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+    fin = ~np.isnan(x)
+    np.testing.assert_array_equal(got[fin], want[fin])
+    assert np.isnan(np.frombuffer((got[~fin].astype(np.uint32) << 16).tobytes(), np.float32)).all()
+
+
+# ---------------------------------------------------------------------------
+# attention (QK^T, scale, key-padding mask, softmax, PV) over packed sequences
+# ---------------------------------------------------------------------------
+def attention64(qkv, cu, H, nh):
+    hd = H // nh
+    out = np.zeros((qkv.shape[0], H))
+    for b in range(len(cu) - 1):
+        s, e = cu[b], cu[b + 1]
+        if e == s:
+            continue
+        for h in range(nh):
+            q = qkv[s:e, h * hd:(h + 1) * hd].astype(np.float64)
+            k = qkv[s:e, H + h * hd:H + (h + 1) * hd].astype(np.float64)
+            v = qkv[s:e, 2 * H + h * hd:2 * H + (h + 1) * hd].astype(np.float64)
+            sc = (q @ k.T) * (1.0 / np.sqrt(hd))
+            p = np.exp(sc - sc.max(1, keepdims=True))
+            out[s:e, h * hd:(h + 1) * hd] = (p / p.sum(1, keepdims=True)) @ v
+    return out
+
+
+@pytest.mark.parametrize("H,nh,lengths", [
+    (384, 12, [1, 2, 31, 32, 33, 127, 128, 129]),
+    (384, 12, [256, 300, 511, 512]),
+    (768, 12, [1, 64, 128, 130, 257]),
+    (64, 2, [5, 17]),
+])
+def test_attention(env, H, nh, lengths):
+    torch, eb, Nn, L = env
+    rng = np.random.default_rng(sum(lengths) + H)
+    T = sum(lengths)
+    qkv = rng.standard_normal((T, 3 * H)).astype(np.float32)
+    cu = np.concatenate([[0], np.cumsum(lengths)]).astype(np.int32)
+    dq, dcu = dev(torch, qkv), dev(torch, cu)
+    dctx = torch.full((T, H), float("nan"), device="cuda")
+    Nn.check(L.ebh_op_attention(vp(dq), vp(dcu), len(lengths), max(lengths), H, nh, vp(dctx),
+                                stream(torch)))
+    torch.cuda.synchronize()
+    np.testing.assert_allclose(dctx.cpu().numpy(), attention64(qkv, cu, H, nh), rtol=0, atol=2e-5)
+
+
+def test_attention_empty_sequence_writes_nothing(env):
+    torch, eb, Nn, L = env
+    H, nh = 384, 12
+    cu = np.array([0, 3, 3, 5], np.int32)            # middle sequence empty
+    qkv = np.random.default_rng(0).standard_normal((5, 3 * H)).astype(np.float32)
+    dctx = torch.zeros((5, H), device="cuda")
+    dq, dcu = dev(torch, qkv), dev(torch, cu)
+    Nn.check(L.ebh_op_attention(vp(dq), vp(dcu), 3, 3, H, nh, vp(dctx),
+                                stream(torch)))
+    torch.cuda.synchronize()
+    np.testing.assert_allclose(dctx.cpu().numpy(), attention64(qkv, cu, H, nh), rtol=0, atol=2e-5)
+
+
+# ---------------------------------------------------------------------------
+# row kernels
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize("H", [64, 384, 768, 1000])
+def test_layer_norm(env, H):
+    torch, eb, Nn, L = env
+    import oracle
+    rng = np.random.default_rng(H)
+    x = (3 * rng.standard_normal((333, H)) + 1).astype(np.float32)
+    g = rng.standard_normal(H).astype(np.float32)
+    b = rng.standard_normal(H).astype(np.float32)
+    dx, dg, db = dev(torch, x), dev(torch, g), dev(torch, b)
+    dy = torch.empty_like(dx)
+    Nn.check(L.ebh_op_layer_norm(vp(dx), vp(dg), vp(db), 333, H,
+                                 ctypes.c_float(1e-12), vp(dy), stream(torch)))
+    Nn.check(L.ebh_op_layer_norm(vp(dx), vp(dg), vp(db), 333, H,
+                                 ctypes.c_float(1e-12), vp(dx), stream(torch)))    # in place
+    torch.cuda.synchronize()
+    want = oracle.layer_norm(x, g, b, 1e-12)
+    np.testing.assert_allclose(dy.cpu().numpy(), want, rtol=0, atol=1e-5)
+    np.testing.assert_array_equal(dx.cpu().numpy(), dy.cpu().numpy())
+
+
+@pytest.mark.parametrize("normalize", [0, 1])
+def test_pool(env, normalize):
+    torch, eb, Nn, L = env
+    H, S = 384, 64
+    lengths = [1, 5, 64, 0, 33]
+    cu = np.concatenate([[0], np.cumsum(lengths)]).astype(np.int32)
+    x = np.random.default_rng(1).standard_normal((cu[-1], H)).astype(np.float32)
+    dout = torch.empty((len(lengths), H), device="cuda")
+    dx, dcu = dev(torch, x), dev(torch, cu)
+    Nn.check(L.ebh_op_pool(vp(dx), vp(dcu), len(lengths), H, S, normalize,
+                           vp(dout), stream(torch)))
+    torch.cuda.synchronize()
+    got = dout.cpu().numpy()
+    for b, n in enumerate(lengths):
+        if n == 0:
+            assert np.isnan(got[b]).all()            # all-masked sequence: NaN, as the reference
+            continue
+        want = x[cu[b]:cu[b + 1]].astype(np.float64).mean(0)
+        if normalize:
+            want = want / max(np.linalg.norm(want), 1e-12)
+        np.testing.assert_allclose(got[b], want, rtol=0, atol=2e-6)
+
+
+def test_pack_with_holes(env):
+    """Masks need not be a prefix: every mask==1 token is kept with its position."""
+    torch, eb, Nn, L = env
+    rng = np.random.default_rng(5)
+    B, S = 37, 300
+    ids = rng.integers(0, 30522, (B, S)).astype(np.int32)
+    mask = (rng.random((B, S)) < 0.6).astype(np.int32)
+    mask[3] = 0
+    mask[4] = 1
+    d = {k: torch.zeros(n, dtype=torch.int32, device="cuda")
+         for k, n in [("counts", B), ("cu", B + 1), ("n", 1), ("tid", B * S), ("tpos", B * S), ("err", 1)]}
+    d["err"].fill_(7)
+    dids, dmask = dev(torch, ids), dev(torch, mask)
+    Nn.check(L.ebh_op_pack(vp(dids), vp(dmask), B, S, vp(d["counts"]),
+                           vp(d["cu"]), vp(d["n"]), vp(d["tid"]), vp(d["tpos"]), vp(d["err"]),
+                           stream(torch)))
+    torch.cuda.synchronize()
+    n = int(d["n"].item())
+    assert n == mask.sum()
+    np.testing.assert_array_equal(d["tid"].cpu().numpy()[:n], ids[mask != 0])
+    np.testing.assert_array_equal(d["tpos"].cpu().numpy()[:n], np.nonzero(mask)[1])
+    np.testing.assert_array_equal(d["cu"].cpu().numpy(), np.concatenate([[0], np.cumsum(mask.sum(1))]))
+    assert int(d["err"].item()) == 0
+
+
+def test_embed_ln_flags_bad_ids(env, weights_for):
+    torch, eb, Nn, L = env
+    import oracle
+    cfg = eb.MINILM_L6
+    w = weights_for(cfg)
+    H, V = cfg.hidden_size, cfg.vocab_size
+    tok = np.array([101, 5, V - 1, 102, V + 3, -2], np.int32)
+    pos = np.array([0, 1, 2, 3, 511, 7], np.int32)
+    T = len(tok)
+    dn = dev(torch, np.array([T], np.int32))
+    derr = torch.zeros(1, dtype=torch.int32, device="cuda")
+    dx = torch.empty((T, H), device="cuda")
+    dw = {k: dev(torch, w[k]) for k in ("embeddings.word_embeddings.weight",
+                                        "embeddings.position_embeddings.weight",
+                                        "embeddings.token_type_embeddings.weight",
+                                        "embeddings.LayerNorm.weight", "embeddings.LayerNorm.bias")}
+    dtok, dpos = dev(torch, tok), dev(torch, pos)
+    Nn.check(L.ebh_op_embed_ln(vp(dtok), vp(dpos), vp(dn), T,
+                               vp(dw["embeddings.word_embeddings.weight"]),
+                               vp(dw["embeddings.position_embeddings.weight"]),
+                               vp(dw["embeddings.token_type_embeddings.weight"]),
+                               vp(dw["embeddings.LayerNorm.weight"]), vp(dw["embeddings.LayerNorm.bias"]),
+                               V, H, ctypes.c_float(1e-12), vp(dx), vp(derr), stream(torch)))
+    torch.cuda.synchronize()
+    assert int(derr.item()) == 1
+    safe = np.where((tok >= 0) & (tok < V), tok, 0)
+    e = (w["embeddings.word_embeddings.weight"][safe] + w["embeddings.position_embeddings.weight"][pos]
+         + w["embeddings.token_type_embeddings.weight"][0])
+    want = oracle.layer_norm(e.astype(np.float32), w["embeddings.LayerNorm.weight"],
+                             w["embeddings.LayerNorm.bias"], 1e-12)
+    np.testing.assert_allclose(dx.cpu().numpy(), want, rtol=0, atol=1e-5)
+
+
+# ---------------------------------------------------------------------------
+# model-level edge cases
+# ---------------------------------------------------------------------------
+_M = {}
+
+
+@pytest.fixture(scope="module")
+def minilm(env, weights_for):
+    torch, eb, Nn, L = env
+    if "m" not in _M:
+        _M["m"] = eb.Model.from_weights(weights_for(eb.MINILM_L6), eb.MINILM_L6, "fp32")
+    return _M["m"]
+
+
+@pytest.fixture(scope="module")
+def orc(weights_for):
+    import oracle
+    from edgebert_amd import synth
+    return oracle.OracleModel(synth.MINILM_L6, weights_for(synth.MINILM_L6))
+
+
+def test_golden_fixtures(env, minilm):
+    with np.load(GOLDEN, allow_pickle=False) as g:
+        for case in ("c1", "c2"):
+            got = minilm.encode_ids(g[f"{case}_ids"], g[f"{case}_mask"], normalize=True)
+            assert np.abs(got - g[f"{case}_out"]).max() <= 1e-4
+            assert cosine_rows(got, g[f"{case}_out"]).min() >= 0.99999
+        got = minilm.forward(g["c1_ids"].astype(np.float32), g["c1_mask"].astype(np.float32))
+        assert np.abs(got - g["c1_pooled"]).max() <= 1e-4
+
+
+def test_empty_batch_and_empty_sequence(env, minilm):
+    torch, eb, Nn, L = env
+    assert minilm.encode_ids(np.zeros((0, 5), np.uint32), np.zeros((0, 5), np.uint32)).shape == (0, 384)
+    out = minilm.encode_ids(np.zeros((3, 0), np.uint32), np.zeros((3, 0), np.uint32), normalize=False)
+    assert out.shape == (3, 384) and (out == 0).all()
+
+
+def test_all_masked_row_is_nan_others_unchanged(env, minilm, orc):
+    ids = np.array([[101, 2000, 3000, 102], [101, 2500, 102, 0], [101, 7, 8, 102]], np.uint32)
+    mask = np.array([[1, 1, 1, 1], [0, 0, 0, 0], [1, 1, 1, 1]], np.uint32)
+    got = minilm.encode_ids(ids, mask, normalize=True)
+    assert np.isnan(got[1]).all()
+    want = orc.encode(ids, mask, normalize=True)
+    assert np.isnan(want[1]).all()
+    assert np.abs(got[[0, 2]] - want[[0, 2]]).max() <= 1e-4
+
+
+def test_mask_with_holes_matches_padded_oracle(env, minilm, orc):
+    """Left padding and holes: positions stay absolute, as in the reference."""
+    rng = np.random.default_rng(9)
+    ids = rng.integers(1000, 30522, (6, 40)).astype(np.float32)
+    mask = (rng.random((6, 40)) < 0.7).astype(np.float32)
+    mask[0, :10] = 0          # left padded
+    mask[:, 5] = 1
+    got = minilm.forward(ids, mask)
+    want = orc.forward(ids, mask)
+    assert np.abs(got - want).max() <= 1e-4
+    assert cosine_rows(got, want).min() >= 0.99999
+
+
+def test_out_of_range_inputs(env, minilm):
+    torch, eb, Nn, L = env
+    ids = np.full((2, 4), 101, np.uint32)
+    mask = np.ones((2, 4), np.uint32)
+    ids[1, 2] = 30522
+    with pytest.raises(eb.EbhError, match="out of range") as e:
+        minilm.encode_ids(ids, mask)
+    assert e.value.code == Nn.EBH_ERR_RANGE
+    with pytest.raises(eb.EbhError, match="max_position_embeddings"):
+        minilm.encode_ids(np.full((1, 513), 101, np.uint32), np.ones((1, 513), np.uint32))
+    with pytest.raises(eb.EbhError, match="not 0 or 1"):
+        minilm.forward(np.full((1, 3), 101, np.float32), np.array([[1, 0.5, 1]], np.float32))
+    # float ids as the reference casts them (`as usize`): 101.7 -> 101, -3 -> 0
+    a = minilm.forward(np.array([[101.7, -3.0, 102.2]], np.float32), np.ones((1, 3), np.float32))
+    b = minilm.forward(np.array([[101, 0, 102]], np.float32), np.ones((1, 3), np.float32))
+    np.testing.assert_array_equal(a, b)
+
+
+def test_device_path_reports_bad_id_on_synchronize(env, minilm):
+    torch, eb, Nn, L = env
+    ids = torch.full((2, 8), 101, dtype=torch.int32, device="cuda")
+    ids[1, 3] = 40000
+    mask = torch.ones_like(ids)
+    out = torch.empty((2, 384), device="cuda")
+    minilm.encode_device(ids.data_ptr(), mask.data_ptr(), 2, 8, out.data_ptr(), True,
+                         torch.cuda.current_stream().cuda_stream)
+    with pytest.raises(eb.EbhError, match="out of range") as e:
+        minilm.synchronize()
+    assert e.value.code == Nn.EBH_ERR_RANGE
+    ids[1, 3] = 2000
+    minilm.encode_device(ids.data_ptr(), mask.data_ptr(), 2, 8, out.data_ptr(), True,
+                         torch.cuda.current_stream().cuda_stream)
+    minilm.synchronize()                             # flag cleared, no error
+    host = minilm.encode_ids(ids.cpu().numpy().astype(np.uint32), mask.cpu().numpy().astype(np.uint32))
+    np.testing.assert_array_equal(out.cpu().numpy(), host)
+
+
+def test_concurrent_callers_and_workspace_growth(env, minilm):
+    """encode(&self) is shared by rayon workers (src/lib.rs:440-451): many host
+    threads on one model give the results of serial calls, across workspace growth."""
+    from edgebert_amd import synth
+    cases = []
+    for i, (B, lo, hi) in enumerate([(3, 4, 10), (40, 8, 128), (2, 300, 512), (17, 2, 60)]):
+        spec = synth.InputSpec(f"t{i}", synth.MINILM_L6, B, hi, lo, hi, 100 + i)
+        ids, mask, _ = synth.make_inputs(spec)
+        cases.append((ids, mask))
+    serial = [minilm.encode_ids(i, m) for i, m in cases]
+    results = {}
+
+    def run(k):
+        for rep in range(3):
+            for j, (i, m) in enumerate(cases):
+                results[(k, rep, j)] = minilm.encode_ids(i, m)
+
+    ts = [threading.Thread(target=run, args=(k,)) for k in range(4)]
+    for t in ts:
+        t.start()
+    for t in ts:
+        t.join()
+    assert len(results) == 4 * 3 * len(cases)
+    for (k, rep, j), v in results.items():
+        np.testing.assert_array_equal(v, serial[j])
+
+
+def test_from_pretrained_path_safetensors(env, tmp_path, weights_for):
+    """config.json + model.safetensors (written by the safetensors library) -> the
+    vectors of the same tensors handed over one by one."""
+    torch, eb, Nn, L = env
+    from safetensors.numpy import save_file
+    from edgebert_amd import synth
+    cfg = synth.TINY
+    w = weights_for(cfg)
+    st = {k: np.ascontiguousarray(v) for k, v in w.items()}
+    st["pooler.dense.weight"] = np.zeros((cfg.hidden_size, cfg.hidden_size), np.float32)
+    save_file(st, str(tmp_path / "model.safetensors"))
+    with open(tmp_path / "config.json", "w") as f:
+        json.dump({"hidden_size": cfg.hidden_size, "num_attention_heads": cfg.num_attention_heads,
+                   "num_hidden_layers": cfg.num_hidden_layers, "intermediate_size": cfg.intermediate_size,
+                   "vocab_size": cfg.vocab_size, "max_position_embeddings": cfg.max_position_embeddings,
+                   "layer_norm_eps": cfg.layer_norm_eps, "hidden_act": "gelu", "model_type": "bert"}, f)
+    m1 = eb.Model.from_pretrained_path(str(tmp_path))
+    m2 = eb.Model.from_weights(w, cfg)
+    ids, mask, _ = synth.make_inputs(synth.InputSpec("t", cfg, 5, 20, 3, 20, 4))
+    np.testing.assert_array_equal(m1.encode_ids(ids, mask), m2.encode_ids(ids, mask))
+    m1.close()
+    m2.close()
+
+
+def test_bf16_minilm_c3(env, weights_for, orc):
+    """bf16 GEMMs at the headline shape: cosine >= 0.999 against the fp32 oracle."""
+    torch, eb, Nn, L = env
+    spec = eb.CONFIGS["c3"]
+    ids, mask, _ = eb.make_inputs(spec)
+    m16 = eb.Model.from_weights(weights_for(spec.model), spec.model, "bf16")
+    got = m16.encode_ids(ids, mask)
+    sel = np.arange(0, spec.batch, 32)
+    want = orc.encode(ids[sel], mask[sel])
+    assert cosine_rows(got[sel], want).min() >= 0.999
+    m16.close()

@@ -1,0 +1,316 @@
+"""Pins of the CPU oracle (``oracle/liboracle.so``), the checker of the HIP path.
+
+Every oracle function is checked against something other than its own
+formula:
+
+* the reference's own unit tests (src/lib.rs:1238-1249 softmax,
+  src/lib.rs:1275-1290 LayerNorm, src/lib.rs:1250-1274 cosine invariants);
+* library routines computed in float64: numpy matmul for the sgemm family,
+  ``torch.nn.functional.layer_norm`` / ``gelu(approximate="tanh")`` /
+  ``softmax``;
+* an independent implementation of the whole encoder:
+  ``transformers.BertModel`` with the tanh GELU and eager attention, loaded
+  with the same HF-named tensors, then masked mean pooling + L2 normalise;
+* invariants of the path: padding invariance (a padded batch equals each
+  sequence run alone), batch-permutation equivariance, S = 1 attention.
+
+CPU only (no GPU marker).
+"""
+import numpy as np
+import pytest
+
+import oracle
+from edgebert_amd import synth
+
+RNG = np.random.default_rng(1234)
+
+
+# ---------------------------------------------------------------------------
+# the reference's unit tests, restated
+# ---------------------------------------------------------------------------
+def test_softmax_reference_unit_test():
+    """src/lib.rs:1238-1249: softmax([1,2,3]) sums to 1 within 1e-6, all > 0."""
+    y = oracle.softmax(np.array([[[[1.0, 2.0, 3.0]]]], np.float32))
+    assert abs(float(y.sum(axis=3)[0, 0, 0]) - 1.0) < 1e-6
+    assert (y > 0).all()
+    e = np.exp(np.array([1.0, 2.0, 3.0]) - 3.0)
+    np.testing.assert_allclose(y.ravel(), e / e.sum(), rtol=1e-6)
+
+
+def test_layer_norm_reference_unit_test():
+    """src/lib.rs:1275-1290: LN([1,2,3,4]), eps 1e-5 -> mean 0, population std 1 (1e-5)."""
+    x = np.array([[[1.0, 2.0, 3.0, 4.0]]], np.float32)
+    y = oracle.layer_norm(x, np.ones(4, np.float32), np.zeros(4, np.float32), 1e-5)
+    assert abs(float(y.mean())) < 1e-5
+    assert abs(float(y.astype(np.float64).std()) - 1.0) < 1e-5
+
+
+def test_cosine_similarity_invariants():
+    """src/lib.rs:1255-1271 and the formula of src/lib.rs:756-789."""
+    for n in (1, 7, 8, 384, 385):
+        a = RNG.standard_normal(n).astype(np.float32)
+        b = RNG.standard_normal(n).astype(np.float32)
+        assert abs(oracle.cosine_similarity(a, a) - 1.0) < 1e-6
+        assert abs(oracle.cosine_similarity(a, b) - oracle.cosine_similarity(b, a)) < 1e-6
+        want = np.dot(a.astype(np.float64), b) / (np.linalg.norm(a.astype(np.float64)) *
+                                                   np.linalg.norm(b.astype(np.float64)) + 1e-8)
+        assert abs(oracle.cosine_similarity(a, b) - want) < 1e-5
+    z = np.zeros(16, np.float32)
+    assert oracle.cosine_similarity(z, z) == 0.0      # 0 / (0 + 1e-8)
+
+
+# ---------------------------------------------------------------------------
+# ops against float64 library routines
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize("m,n,k", [(1, 1, 1), (7, 19, 13), (6, 16, 32), (37, 100, 384),
+                                   (130, 384, 1536), (5, 0, 3), (3, 5, 0)])
+def test_sgemm_vs_numpy(m, n, k):
+    a = RNG.standard_normal((m, k)).astype(np.float32)
+    b = RNG.standard_normal((k, n)).astype(np.float32)
+    got = oracle.sgemm(a, b) if n else np.zeros((m, 0), np.float32)
+    want = a.astype(np.float64) @ b.astype(np.float64)
+    np.testing.assert_allclose(got, want, rtol=1e-5, atol=1e-5 * np.sqrt(max(k, 1)))
+
+
+@pytest.mark.parametrize("batch", [1, 4, 5, 9])
+def test_matmul_3d_2d_vs_numpy(batch):
+    """matmul_3d_2d (src/lib.rs:795-849), sequential (B<=4) and parallel branches."""
+    a = RNG.standard_normal((batch, 11, 24)).astype(np.float32)
+    w = RNG.standard_normal((24, 40)).astype(np.float32)
+    np.testing.assert_allclose(oracle.matmul_3d_2d(a, w),
+                               np.einsum("bmk,kn->bmn", a.astype(np.float64), w), rtol=1e-5,
+                               atol=1e-5)
+
+
+@pytest.mark.parametrize("B,h", [(1, 2), (3, 4)])
+def test_matmul_4d_vs_numpy(B, h):
+    """matmul_4d (src/lib.rs:898-956), <= 8 and > 8 (batch*heads) branches."""
+    a = RNG.standard_normal((B, h, 9, 5)).astype(np.float32)
+    b = RNG.standard_normal((B, h, 5, 13)).astype(np.float32)
+    np.testing.assert_allclose(oracle.matmul_4d(a, b), a.astype(np.float64) @ b, rtol=1e-5,
+                               atol=1e-5)
+
+
+def test_softmax_vs_torch():
+    import torch
+    x = (4 * RNG.standard_normal((3, 2, 17, 33))).astype(np.float32)
+    want = torch.softmax(torch.from_numpy(x).double(), dim=-1).numpy()
+    np.testing.assert_allclose(oracle.softmax(x), want, rtol=1e-5, atol=1e-7)
+
+
+def test_mask_then_softmax():
+    """apply_attention_mask (src/lib.rs:872-896): mask==0 keys get exactly zero
+    weight; a row whose keys are all masked is NaN (exp(-inf - -inf))."""
+    B, nh, S = 2, 3, 6
+    scores = RNG.standard_normal((B, nh, S, S)).astype(np.float32)
+    mask = np.ones((B, S), np.float32)
+    mask[0, 4:] = 0.0
+    mask[1, :] = 0.0
+    w = oracle.softmax(oracle.apply_attention_mask(scores, mask))
+    assert (w[0, :, :, 4:] == 0.0).all()
+    np.testing.assert_allclose(w[0].sum(-1), 1.0, rtol=1e-6)
+    e = np.exp(scores[0, :, :, :4].astype(np.float64) - scores[0, :, :, :4].max(-1, keepdims=True))
+    np.testing.assert_allclose(w[0, :, :, :4], e / e.sum(-1, keepdims=True), rtol=1e-5)
+    assert np.isnan(w[1]).all()
+
+
+def test_gelu_vs_torch_tanh():
+    """gelu (src/lib.rs:958-978) is the tanh approximation, whatever hidden_act says."""
+    import torch
+    x = np.concatenate([np.linspace(-12, 12, 4001), 3 * RNG.standard_normal(2000)]).astype(np.float32)
+    want = torch.nn.functional.gelu(torch.from_numpy(x).double(), approximate="tanh").numpy()
+    np.testing.assert_allclose(oracle.gelu(x), want, rtol=2e-6, atol=2e-7)
+    erf_gelu = torch.nn.functional.gelu(torch.from_numpy(x).double()).numpy()
+    assert np.abs(oracle.gelu(x) - erf_gelu).max() > 1e-4  # and not the erf form
+
+
+@pytest.mark.parametrize("H,eps", [(4, 1e-5), (64, 1e-12), (384, 1e-12), (768, 1e-12), (33, 1e-3)])
+def test_layer_norm_vs_torch(H, eps):
+    import torch
+    x = (RNG.standard_normal((50, H)) * 3 + 0.5).astype(np.float32)
+    g = RNG.standard_normal(H).astype(np.float32)
+    b = RNG.standard_normal(H).astype(np.float32)
+    want = torch.nn.functional.layer_norm(torch.from_numpy(x).double(), (H,),
+                                          torch.from_numpy(g).double(),
+                                          torch.from_numpy(b).double(), eps).numpy()
+    np.testing.assert_allclose(oracle.layer_norm(x, g, b, eps), want, rtol=1e-5, atol=2e-5)
+
+
+def test_mean_pool_and_normalize():
+    """mean_pool (src/lib.rs:993-1010) and the normalise tail (src/lib.rs:605-612)."""
+    B, S, H = 3, 5, 8
+    h = RNG.standard_normal((B, S, H)).astype(np.float32)
+    mask = np.array([[1, 1, 1, 0, 0], [1, 1, 1, 1, 1], [0, 0, 0, 0, 0]], np.float32)
+    h[0, :3] = h[0, 0]                       # constant over the real tokens
+    got = oracle.mean_pool(h, mask)
+    np.testing.assert_allclose(got[0], h[0, 0], rtol=1e-6)
+    np.testing.assert_allclose(got[1], h[1].astype(np.float64).mean(0), rtol=1e-5, atol=1e-6)
+    assert (got[2] == 0.0).all()             # count clamps to 1, sum is 0
+    x = got.copy()
+    oracle.normalize_rows(x)
+    np.testing.assert_allclose(np.linalg.norm(x[:2].astype(np.float64), axis=1), 1.0, rtol=1e-6)
+    assert (x[2] == 0.0).all()               # x / max(0, 1e-12)
+
+
+# ---------------------------------------------------------------------------
+# the whole encoder against transformers.BertModel
+# ---------------------------------------------------------------------------
+def hf_encode(cfg, weights, ids, mask, normalize=True, hidden_states=False):
+    """transformers' BERT (tanh GELU, eager attention) + masked mean + F.normalize."""
+    import torch
+    from transformers import BertConfig as HFConfig, BertModel
+    hcfg = HFConfig(vocab_size=cfg.vocab_size, hidden_size=cfg.hidden_size,
+                    num_hidden_layers=cfg.num_hidden_layers,
+                    num_attention_heads=cfg.num_attention_heads,
+                    intermediate_size=cfg.intermediate_size,
+                    max_position_embeddings=cfg.max_position_embeddings,
+                    type_vocab_size=cfg.type_vocab_size, layer_norm_eps=cfg.layer_norm_eps,
+                    hidden_act="gelu_pytorch_tanh", attn_implementation="eager",
+                    hidden_dropout_prob=0.0, attention_probs_dropout_prob=0.0)
+    model = BertModel(hcfg, add_pooling_layer=False).eval()
+    sd = {k: torch.from_numpy(np.ascontiguousarray(v)) for k, v in weights.items()}
+    missing, unexpected = model.load_state_dict(sd, strict=False)
+    assert not unexpected and all("position_ids" in k for k in missing), (missing, unexpected)
+    with torch.no_grad():
+        t_ids = torch.from_numpy(np.asarray(ids, np.int64))
+        t_mask = torch.from_numpy(np.asarray(mask, np.int64))
+        out = model(input_ids=t_ids, attention_mask=t_mask,
+                    token_type_ids=torch.zeros_like(t_ids), output_hidden_states=hidden_states)
+        h = out.last_hidden_state.double()
+        m = t_mask.double().unsqueeze(-1)
+        pooled = (h * m).sum(1) / m.sum(1).clamp(min=1.0)
+        if normalize:
+            pooled = torch.nn.functional.normalize(pooled, dim=-1, eps=1e-12)
+    res = pooled.float().numpy()
+    if hidden_states:
+        return res, [s.numpy() for s in out.hidden_states]
+    return res
+
+
+def _tiny_inputs(B=4, S=16, seed=7):
+    spec = synth.InputSpec("tiny", synth.TINY, B, S, 1, S, seed)
+    return synth.make_inputs(spec)
+
+
+def test_tiny_encoder_trace_vs_transformers(weights_for):
+    """Hidden state after the embedding LN and after every layer, padded batch."""
+    cfg = synth.TINY
+    w = weights_for(cfg)
+    ids, mask, _ = _tiny_inputs()
+    om = oracle.OracleModel(cfg, w)
+    pooled, trace = om.forward_trace(ids.astype(np.float32), mask.astype(np.float32))
+    want, hs = hf_encode(cfg, w, ids, mask, normalize=False, hidden_states=True)
+    assert len(hs) == cfg.num_hidden_layers + 1
+    for i, h in enumerate(hs):
+        np.testing.assert_allclose(trace[i], h, rtol=1e-4, atol=2e-5, err_msg=f"hidden state {i}")
+    np.testing.assert_allclose(pooled, want, rtol=1e-4, atol=1e-5)
+
+
+@pytest.mark.parametrize("cname", ["c1", "c2"])
+def test_minilm_encode_vs_transformers(weights_for, cname):
+    """c1 whole; c2 on its first 8 sequences (padded, key-padding mask)."""
+    spec = synth.CONFIGS[cname]
+    w = weights_for(spec.model)
+    ids, mask, _ = synth.make_inputs(spec)
+    ids, mask = ids[:8], mask[:8]
+    got = oracle.OracleModel(spec.model, w).encode(ids, mask, normalize=True)
+    want = hf_encode(spec.model, w, ids, mask)
+    cos = (got.astype(np.float64) * want).sum(1) / (np.linalg.norm(got.astype(np.float64), axis=1)
+                                                    * np.linalg.norm(want.astype(np.float64), axis=1))
+    assert np.abs(got - want).max() <= 1e-5
+    assert cos.min() >= 0.999999
+
+
+def test_bert_base_layer_vs_transformers():
+    """head_dim 64 (BERT-base shape), cut to 2 layers and a 512-row vocab to stay fast."""
+    cfg = synth.BertConfig(hidden_size=768, num_attention_heads=12, num_hidden_layers=2,
+                           intermediate_size=3072, vocab_size=1200, max_position_embeddings=128)
+    w = synth.make_weights(cfg)
+    spec = synth.InputSpec("bb", cfg, 3, 40, 5, 40, 11)
+    ids, mask, _ = synth.make_inputs(spec)
+    got = oracle.OracleModel(cfg, w).encode(ids, mask, normalize=True)
+    want = hf_encode(cfg, w, ids, mask)
+    assert np.abs(got - want).max() <= 1e-5
+
+
+# ---------------------------------------------------------------------------
+# invariants of the path
+# ---------------------------------------------------------------------------
+def test_padding_invariance_c2(weights_for):
+    """A padded batch equals each sequence run alone (mask-0 tokens never reach
+    a mask-1 output): the property the GPU path's token packing relies on."""
+    spec = synth.CONFIGS["c2"]
+    w = weights_for(spec.model)
+    ids, mask, lengths = synth.make_inputs(spec)
+    ids, mask = ids[:6], mask[:6]
+    om = oracle.OracleModel(spec.model, w)
+    padded = om.encode(ids, mask, normalize=True)
+    alone = om.encode_unpadded(ids, mask, normalize=True)
+    np.testing.assert_allclose(padded, alone, rtol=0, atol=2e-6)
+
+
+def test_batch_permutation_equivariance(weights_for):
+    cfg = synth.TINY
+    om = oracle.OracleModel(cfg, weights_for(cfg))
+    ids, mask, _ = _tiny_inputs(B=6)
+    perm = np.array([3, 0, 5, 1, 4, 2])
+    a = om.encode(ids, mask)
+    b = om.encode(ids[perm], mask[perm])
+    np.testing.assert_array_equal(a[perm], b)
+
+
+def test_single_token_attention_is_value(weights_for):
+    """S = 1: softmax over one key is 1, so the context is V and the encoder
+    reduces to per-token dense algebra, computed here in float64."""
+    cfg = synth.TINY
+    w = weights_for(cfg)
+    tid = 777
+    got = oracle.OracleModel(cfg, w).forward(np.array([[tid]], np.float32),
+                                              np.ones((1, 1), np.float32))[0]
+    f = lambda k: w[k].astype(np.float64)
+
+    def ln(x, p):
+        mu = x.mean()
+        return (x - mu) / np.sqrt(((x - mu) ** 2).mean() + cfg.layer_norm_eps) * f(p + ".weight") + f(p + ".bias")
+
+    def gelu(x):
+        return 0.5 * x * (1 + np.tanh(0.7978845608 * (x + 0.044715 * x ** 3)))
+
+    x = ln(f("embeddings.word_embeddings.weight")[tid] + f("embeddings.position_embeddings.weight")[0]
+           + f("embeddings.token_type_embeddings.weight")[0], "embeddings.LayerNorm")
+    for i in range(cfg.num_hidden_layers):
+        p = f"encoder.layer.{i}."
+        v = f(p + "attention.self.value.weight") @ x + f(p + "attention.self.value.bias")
+        a = ln(f(p + "attention.output.dense.weight") @ v + f(p + "attention.output.dense.bias") + x,
+               p + "attention.output.LayerNorm")
+        u = gelu(f(p + "intermediate.dense.weight") @ a + f(p + "intermediate.dense.bias"))
+        x = ln(f(p + "output.dense.weight") @ u + f(p + "output.dense.bias") + a, p + "output.LayerNorm")
+    np.testing.assert_allclose(got, x, rtol=1e-4, atol=1e-5)
+
+
+def test_all_masked_row_is_nan(weights_for):
+    """An all-zero mask row: every score is -inf, softmax gives NaN and so does
+    the pooled vector (the reference's behaviour); other rows are unaffected."""
+    cfg = synth.TINY
+    om = oracle.OracleModel(cfg, weights_for(cfg))
+    ids, mask, _ = _tiny_inputs(B=3)
+    mask2 = mask.copy()
+    mask2[1] = 0
+    out = om.forward(ids.astype(np.float32), mask2.astype(np.float32))
+    assert np.isnan(out[1]).all()
+    ref = om.forward(ids.astype(np.float32), mask.astype(np.float32))
+    np.testing.assert_array_equal(out[[0, 2]], ref[[0, 2]])
+
+
+def test_oracle_errors(weights_for):
+    cfg = synth.TINY
+    om = oracle.OracleModel(cfg, weights_for(cfg))
+    with pytest.raises(oracle.OracleError, match="out of range"):
+        om.forward(np.array([[cfg.vocab_size]], np.float32), np.ones((1, 1), np.float32))
+    with pytest.raises(oracle.OracleError, match="max_position"):
+        S = cfg.max_position_embeddings + 1
+        om.forward(np.ones((1, S), np.float32), np.ones((1, S), np.float32))
+    w = dict(weights_for(cfg))
+    del w["encoder.layer.1.output.dense.bias"]
+    with pytest.raises(oracle.OracleError, match="not found"):
+        oracle.OracleModel(cfg, w)
