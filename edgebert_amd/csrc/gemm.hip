@@ -18,6 +18,8 @@
 // each lane fetches its four operands with one 16-byte LDS read and MFMA q
 // (q = 0..3) uses k = 4h + q.  A and W use the same map, so the products
 // summed are exactly those of the dot product.
+#include <algorithm>
+
 #include "kernels.hpp"
 
 namespace ebh {
@@ -48,18 +50,25 @@ __device__ __forceinline__ float epilogue(float acc, float bias, const float* R,
 }
 
 // ---------------------------------------------------------------------------
-// fp32: v_mfma_f32_32x32x2_f32
+// fp32: v_mfma_f32_32x32x2_f32.
+// NT = 64 * WAVES_M * WAVES_N threads; wave (wm, wn) owns the (BM/WAVES_M) x
+// (BN/WAVES_N) sub-tile as FM x FN blocks of 32x32.  KFULL: the launcher has
+// checked that K is a multiple of BK, so the k-tile loads carry no guard.
 // ---------------------------------------------------------------------------
-template <int BM, int BN, int BK, int WAVES_M, int WAVES_N, int EPI>
-__global__ __launch_bounds__(256) void gemm_f32_kernel(GemmArgs p) {
-    static_assert(WAVES_M * WAVES_N == 4, "4 waves per workgroup");
+template <int BM, int BN, int BK, int WAVES_M, int WAVES_N, int EPI, bool KFULL>
+__global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_f32_kernel(GemmArgs p) {
+    constexpr int NT = 64 * WAVES_M * WAVES_N;
     constexpr int WM = BM / WAVES_M, WN = BN / WAVES_N;
     constexpr int FM = WM / 32, FN = WN / 32;
+    static_assert(FM * 32 == WM && FN * 32 == WN, "wave tile must be whole 32x32 blocks");
     constexpr int LDS_STRIDE = BK + 4;            // floats; 16-B aligned rows, conflict-free b128 reads
     constexpr int KF4 = BK / 4;                   // float4 per tile row
-    constexpr int A_LD = BM * KF4 / 256;          // float4 loads per thread per k-tile
-    constexpr int W_LD = BN * KF4 / 256;
-    static_assert(A_LD * 256 == BM * KF4 && W_LD * 256 == BN * KF4, "tile/thread mismatch");
+    constexpr int A_TOT = BM * KF4, W_TOT = BN * KF4;   // float4 per k-tile
+    constexpr int A_LD = (A_TOT + NT - 1) / NT;   // float4 loads per thread per k-tile
+    constexpr int W_LD = (W_TOT + NT - 1) / NT;
+    // Whether load i of this thread exists (only the last one can be partial).
+    auto a_on = [&](int i) { return A_TOT % NT == 0 || i + 1 < A_LD || (int)threadIdx.x + NT * i < A_TOT; };
+    auto w_on = [&](int i) { return W_TOT % NT == 0 || i + 1 < W_LD || (int)threadIdx.x + NT * i < W_TOT; };
 
     __shared__ __attribute__((aligned(16))) float As[2][BM * LDS_STRIDE];
     __shared__ __attribute__((aligned(16))) float Ws[2][BN * LDS_STRIDE];
@@ -84,17 +93,17 @@ __global__ __launch_bounds__(256) void gemm_f32_kernel(GemmArgs p) {
     int a_lds[A_LD], w_lds[W_LD], a_col[A_LD], w_col[W_LD];
 #pragma unroll
     for (int i = 0; i < A_LD; ++i) {
-        int idx = tid + 256 * i, r = idx / KF4, c = idx % KF4;
+        int idx = tid + NT * i, r = idx / KF4, c = idx % KF4;
         int gr = min(m0 + r, M - 1);
-        a_src[i] = A + (int64_t)gr * p.lda;
+        a_src[i] = A + (int64_t)gr * p.lda + c * 4;
         a_col[i] = c * 4;
         a_lds[i] = r * LDS_STRIDE + c * 4;
     }
 #pragma unroll
     for (int i = 0; i < W_LD; ++i) {
-        int idx = tid + 256 * i, r = idx / KF4, c = idx % KF4;
+        int idx = tid + NT * i, r = idx / KF4, c = idx % KF4;
         int gr = min(n0 + r, N - 1);
-        w_src[i] = W + (int64_t)gr * p.ldw;
+        w_src[i] = W + (int64_t)gr * p.ldw + c * 4;
         w_col[i] = c * 4;
         w_lds[i] = r * LDS_STRIDE + c * 4;
     }
@@ -103,20 +112,28 @@ __global__ __launch_bounds__(256) void gemm_f32_kernel(GemmArgs p) {
     auto gload = [&](int k0) {
 #pragma unroll
         for (int i = 0; i < A_LD; ++i) {
-            int k = k0 + a_col[i];
-            ra[i] = k < K ? *reinterpret_cast<const float4*>(a_src[i] + k) : make_float4(0, 0, 0, 0);
+            if (!a_on(i)) continue;
+            if (KFULL || k0 + a_col[i] < K)
+                ra[i] = *reinterpret_cast<const float4*>(a_src[i] + k0);
+            else
+                ra[i] = make_float4(0, 0, 0, 0);
         }
 #pragma unroll
         for (int i = 0; i < W_LD; ++i) {
-            int k = k0 + w_col[i];
-            rw[i] = k < K ? *reinterpret_cast<const float4*>(w_src[i] + k) : make_float4(0, 0, 0, 0);
+            if (!w_on(i)) continue;
+            if (KFULL || k0 + w_col[i] < K)
+                rw[i] = *reinterpret_cast<const float4*>(w_src[i] + k0);
+            else
+                rw[i] = make_float4(0, 0, 0, 0);
         }
     };
     auto lstore = [&](int buf) {
 #pragma unroll
-        for (int i = 0; i < A_LD; ++i) *reinterpret_cast<float4*>(&As[buf][a_lds[i]]) = ra[i];
+        for (int i = 0; i < A_LD; ++i)
+            if (a_on(i)) *reinterpret_cast<float4*>(&As[buf][a_lds[i]]) = ra[i];
 #pragma unroll
-        for (int i = 0; i < W_LD; ++i) *reinterpret_cast<float4*>(&Ws[buf][w_lds[i]]) = rw[i];
+        for (int i = 0; i < W_LD; ++i)
+            if (w_on(i)) *reinterpret_cast<float4*>(&Ws[buf][w_lds[i]]) = rw[i];
     };
 
     v16f acc[FM][FN];
@@ -177,6 +194,395 @@ __global__ __launch_bounds__(256) void gemm_f32_kernel(GemmArgs p) {
                 if (row < M)
                     p.C[(int64_t)row * p.ldc + col] =
                         epilogue<EPI>(acc[i][j][r], bcol, p.R, p.ldr, row, col);
+            }
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// fp32, direct-to-LDS: the main fp32 kernel when K is a multiple of BK and
+// every row start is 16-byte aligned.
+//
+// Global -> LDS: global_load_lds_dwordx4 (gfx950) moves each lane's 16 bytes
+// straight into LDS, so no VGPRs or ds_write instructions stage the tiles.
+// One such instruction fills 64 consecutive 16-byte LDS chunks per wave, so
+// the tiles are unpadded [rows][BK] and a bank-conflict-free read order comes
+// from an XOR swizzle of the 16-byte chunk within its row instead:
+//   LDS chunk of (row r, k-chunk c) = r * CPR + (c ^ swz(r)),  CPR = BK / 4,
+// and each lane loads the global chunk that belongs at its LDS position.
+// swz spreads any 8 consecutive rows (32 LDS banks) and any 16 consecutive
+// rows (64 banks) over distinct banks for the fragment reads below, where 32
+// lanes read 32 consecutive rows at one k-chunk.
+//
+// Pipeline (two LDS stages, one barrier per k-tile): after the barrier a wave
+// reads all of k-tile kt's fragments into registers, then issues the loads of
+// tile kt+1 into the other stage, then runs the MFMAs of tile kt while those
+// loads land.  The barrier (which waits for the wave's own loads) both
+// publishes tile kt+1 and retires every read of the stage it overwrites.
+// ---------------------------------------------------------------------------
+// One lane's 16 bytes from global memory into LDS (global_load_lds_dwordx4);
+// lds must be the same for every lane of the wave, lane l lands at lds + 16*l bytes.
+__device__ __forceinline__ void load_lds16(const float* g, float* lds) {
+    __builtin_amdgcn_global_load_lds(g, lds, 16, 0, 0);
+}
+
+template <int CPR>
+__device__ __forceinline__ int chunk_swizzle(int r) {
+    static_assert(CPR == 4 || CPR == 8, "BK must be 16 or 32");
+    if constexpr (CPR == 8) return (r & 7) ^ ((r >> 3) & 1);
+    else return ((r >> 1) & 3) ^ ((r >> 3) & 1);
+}
+
+template <int BM, int BN, int BK, int WAVES_M, int WAVES_N, int EPI>
+__global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_f32_dtl_kernel(GemmArgs p) {
+    constexpr int NT = 64 * WAVES_M * WAVES_N;
+    constexpr int WM = BM / WAVES_M, WN = BN / WAVES_N;
+    constexpr int FM = WM / 32, FN = WN / 32;
+    static_assert(FM * 32 == WM && FN * 32 == WN, "wave tile must be whole 32x32 blocks");
+    constexpr int CPR = BK / 4;                   // 16-byte chunks per tile row
+    constexpr int KS = BK / 8;                    // 8-wide k slices per tile
+    constexpr int A_CH = BM * CPR, W_CH = BN * CPR;         // 16-byte chunks per tile
+    constexpr int LA = (A_CH + NT - 1) / NT, LW = (W_CH + NT - 1) / NT;  // loads per thread
+    static_assert(A_CH % 64 == 0 && W_CH % 64 == 0, "a load instruction fills 64 chunks per wave");
+
+    __shared__ __attribute__((aligned(16))) float As[2][BM * BK];
+    __shared__ __attribute__((aligned(16))) float Ws[2][BN * BK];
+
+    const int M = p.M_dev ? *p.M_dev : p.M_max;
+    const int ntiles_n = (p.N + BN - 1) / BN;
+    int mt, nt;
+    tile_coords(ntiles_n, mt, nt);
+    const int m0 = mt * BM, n0 = nt * BN;
+    if (m0 >= M) return;  // uniform over the workgroup
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wm = wave / WAVES_N, wn = wave % WAVES_N;
+    const int l32 = lane & 31, half = lane >> 5;
+    const int N = p.N;
+    const float* __restrict__ A = static_cast<const float*>(p.A);
+    const float* __restrict__ W = static_cast<const float*>(p.W);
+
+    // Global source of each load: LDS chunk P = i*NT + tid holds row P / CPR,
+    // k-chunk (P % CPR) ^ swz(row).  Rows past M / N are clamped (loaded, never stored).
+    const float* a_src[LA];
+    const float* w_src[LW];
+#pragma unroll
+    for (int i = 0; i < LA; ++i) {
+        const int P = i * NT + tid, r = P / CPR, c = (P % CPR) ^ chunk_swizzle<CPR>(r);
+        a_src[i] = A + (int64_t)min(m0 + r, M - 1) * p.lda + c * 4;
+    }
+#pragma unroll
+    for (int i = 0; i < LW; ++i) {
+        const int P = i * NT + tid, r = P / CPR, c = (P % CPR) ^ chunk_swizzle<CPR>(r);
+        w_src[i] = W + (int64_t)min(n0 + r, N - 1) * p.ldw + c * 4;
+    }
+    // Wave-uniform LDS destination of load i: chunks i*NT + wave*64 .. +63.
+    // The last load instruction may cover only part of the tile: whole waves skip it.
+    auto issue = [&](int stage, int k0) {
+#pragma unroll
+        for (int i = 0; i < LA; ++i)
+            if (A_CH % NT == 0 || i * NT + wave * 64 < A_CH)
+                load_lds16(a_src[i] + k0, &As[stage][(i * NT + wave * 64) * 4]);
+#pragma unroll
+        for (int i = 0; i < LW; ++i)
+            if (W_CH % NT == 0 || i * NT + wave * 64 < W_CH)
+                load_lds16(w_src[i] + k0, &Ws[stage][(i * NT + wave * 64) * 4]);
+    };
+
+    // Fragment reads: rows (wave base + 32*i + l32) are 32-aligned, so the swizzle
+    // depends on l32 only.
+    const int sw = chunk_swizzle<CPR>(l32);
+    int koff[KS];
+#pragma unroll
+    for (int s = 0; s < KS; ++s) koff[s] = 4 * ((2 * s + half) ^ sw);
+    const int a_row = (wm * WM + l32) * BK, w_row = (wn * WN + l32) * BK;
+
+    v16f acc[FM][FN];
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+
+    const int nk = p.K / BK;
+    issue(0, 0);
+    for (int kt = 0; kt < nk; ++kt) {
+        const int cur = kt & 1;
+        __syncthreads();
+        v4f af[KS][FM], wf[KS][FN];
+#pragma unroll
+        for (int s = 0; s < KS; ++s) {
+#pragma unroll
+            for (int i = 0; i < FM; ++i)
+                af[s][i] = *reinterpret_cast<const v4f*>(&As[cur][a_row + i * 32 * BK + koff[s]]);
+#pragma unroll
+            for (int j = 0; j < FN; ++j)
+                wf[s][j] = *reinterpret_cast<const v4f*>(&Ws[cur][w_row + j * 32 * BK + koff[s]]);
+        }
+        if (kt + 1 < nk) issue(cur ^ 1, (kt + 1) * BK);
+#pragma unroll
+        for (int s = 0; s < KS; ++s)
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+#pragma unroll
+                for (int i = 0; i < FM; ++i)
+#pragma unroll
+                    for (int j = 0; j < FN; ++j)
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(af[s][i][q], wf[s][j][q],
+                                                                         acc[i][j], 0, 0, 0);
+    }
+
+#pragma unroll
+    for (int j = 0; j < FN; ++j) {
+        const int col = n0 + wn * WN + j * 32 + l32;
+        if (col >= N) continue;
+        const float bcol = p.bias[col];
+#pragma unroll
+        for (int i = 0; i < FM; ++i) {
+            const int rbase = m0 + wm * WM + i * 32 + 4 * half;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int row = rbase + 8 * (r >> 2) + (r & 3);
+                if (row < M)
+                    p.C[(int64_t)row * p.ldc + col] =
+                        epilogue<EPI>(acc[i][j][r], bcol, p.R, p.ldr, row, col);
+            }
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// fp32, persistent: one workgroup per CU walks a strided list of 128x128 C
+// tiles, flattening (tile, k-tile) into one pipelined loop, so the next tile's
+// first loads overlap the current tile's last MFMAs and epilogue.
+//
+// Loads use global_load_lds_dwordx4 issued from inline asm: the compiler's
+// wait-count tracking does not see them, so it does not force every LDS read
+// to wait for every outstanding LDS load; the loop waits explicitly instead
+// (vmcnt(0) + barrier at the top of each k-tile).  That lets a wave read the
+// fragments of k-slice s+1 while the MFMAs of slice s run.  M0 (the LDS
+// destination base of the instruction) is saved and restored inside the asm.
+//
+// LDS: two stages of [BM][BK] + [BN][BK] floats, 16-byte chunks XOR-swizzled
+// within each row (conflict-free fragment reads, see chunk_swizzle).
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ void load_lds16_async(const float* g, const float* lds) {
+    const uint32_t base = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)lds);
+    uint32_t saved;
+    asm volatile(
+        "s_mov_b32 %0, m0\n\t"
+        "s_mov_b32 m0, %2\n\t"
+        "s_nop 0\n\t"
+        "global_load_lds_dwordx4 %1, off\n\t"
+        "s_mov_b32 m0, %0"
+        : "=&s"(saved)
+        : "v"(g), "s"(base)
+        : "memory");
+}
+
+// Every load this wave issued has landed in LDS and every LDS read has
+// returned; then the workgroup barrier.
+__device__ __forceinline__ void wait_all_then_barrier() {
+    asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
+template <int CPR>
+__device__ __forceinline__ int chunk_swizzle16(int r) {
+    if constexpr (CPR == 16) return r & 15;
+    else return chunk_swizzle<CPR>(r);
+}
+
+// Only LDS reads / writes of this wave are outstanding, then the barrier (the
+// next k-tile's loads may still be landing in the other stage).
+__device__ __forceinline__ void wait_lds_then_barrier() {
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
+// tanh-form GELU of the reference (constants of src/lib.rs:151-152) with
+// tanh(u) = 1 - 2 / (1 + e^(2u)) on the hardware exp2 and reciprocal
+// (|error| of tanh below 2e-7; e^(2u) = inf gives 1, 0 gives -1).
+__device__ __forceinline__ float gelu_tanh_fast(float val) {
+    const float SQRT_2_OVER_PI = 0.7978845608f;
+    const float GELU_COEFF = 0.044715f;
+    const float inner = SQRT_2_OVER_PI * (val + GELU_COEFF * (val * val * val));
+    const float e = __builtin_amdgcn_exp2f(inner * 2.8853900817779268f);  // e^(2u)
+    const float t = 1.0f - 2.0f * __builtin_amdgcn_rcpf(1.0f + e);
+    return val * 0.5f * (1.0f + t);
+}
+
+template <int BM, int BN, int BK, int WAVES_M, int WAVES_N, int EPI>
+__global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_f32_persistent_kernel(GemmArgs p) {
+    constexpr int NT = 64 * WAVES_M * WAVES_N;
+    constexpr int WM = BM / WAVES_M, WN = BN / WAVES_N;
+    constexpr int FM = WM / 32, FN = WN / 32;
+    static_assert(FM * 32 == WM && FN * 32 == WN, "wave tile must be whole 32x32 blocks");
+    constexpr int CPR = BK / 4;                   // 16-byte chunks per tile row
+    constexpr int KS = BK / 8;                    // 8-wide k slices per k-tile
+    constexpr int A_CH = BM * CPR, W_CH = BN * CPR;
+    constexpr int LA = (A_CH + NT - 1) / NT, LW = (W_CH + NT - 1) / NT;
+    static_assert(A_CH % 64 == 0 && W_CH % 64 == 0, "a load instruction fills 64 chunks per wave");
+    constexpr int STAGE = (BM + BN) * BK;         // floats per LDS stage: A rows, then W rows
+    constexpr int NW = WAVES_M * WAVES_N;
+    static_assert(NW * 32 * WN <= STAGE, "each wave transposes 32 C rows at a time through one stage");
+    constexpr int C4 = WN / 4;                    // float4 per wave-tile row
+    constexpr int RPP = 64 / C4;                  // wave-tile rows per float4 pass
+    static_assert(C4 * RPP == 64 && 32 % RPP == 0, "epilogue pass shape");
+    constexpr int NPB = 32 / RPP;                 // float4 passes per 32-row block
+    constexpr int NP = FM * NPB;                  // float4 passes per lane
+
+    __shared__ __attribute__((aligned(16))) float smem[2 * STAGE];
+
+    const int M = p.M_dev ? *p.M_dev : p.M_max;
+    const int N = p.N;
+    const int ntiles_n = (N + BN - 1) / BN;
+    const int ntiles = ((M + BM - 1) / BM) * ntiles_n;
+    const int nk = p.K / BK;
+    // Workgroup b runs on XCD b % 8: renumber so each XCD's workgroups take
+    // consecutive tiles (N-fastest), which share A row panels in that XCD's L2.
+    const int G = gridDim.x;
+    const int wg = (G & 7) == 0 ? (blockIdx.x & 7) * (G >> 3) + (blockIdx.x >> 3) : blockIdx.x;
+    const int my_tiles = wg < ntiles ? (ntiles - wg + G - 1) / G : 0;
+    const int total = my_tiles * nk;
+    if (total == 0) return;  // uniform over the workgroup
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wm = wave / WAVES_N, wn = wave % WAVES_N;
+    const int l32 = lane & 31, half = lane >> 5;
+    const float* __restrict__ A = static_cast<const float*>(p.A);
+    const float* __restrict__ W = static_cast<const float*>(p.W);
+
+    // This lane's share of each k-tile load: row and swizzled k-chunk of LDS chunk i*NT + tid.
+    constexpr int NL = LA + LW;                   // load instructions per k-tile
+    int l_r[NL], l_c[NL];
+#pragma unroll
+    for (int i = 0; i < NL; ++i) {
+        const int P = (i < LA ? i : i - LA) * NT + tid;
+        l_r[i] = P / CPR;
+        l_c[i] = 4 * ((P % CPR) ^ chunk_swizzle16<CPR>(P / CPR));
+    }
+    // Source pointers of the next k-tile to load (iteration `nit`), advanced by BK
+    // per k-tile and recomputed when that k-tile starts a new C tile.
+    const float* src[NL];
+    int nit = 0;
+    auto point_at = [&](int it) {
+        const int t = wg + (it / nk) * G, kt = it - (it / nk) * nk;
+        const int mt = t / ntiles_n, m0 = mt * BM, n0 = (t - mt * ntiles_n) * BN;
+#pragma unroll
+        for (int i = 0; i < NL; ++i)
+            src[i] = i < LA ? A + (int64_t)min(m0 + l_r[i], M - 1) * p.lda + kt * BK + l_c[i]
+                            : W + (int64_t)min(n0 + l_r[i], N - 1) * p.ldw + kt * BK + l_c[i];
+    };
+    // Every load of k-tile `nit` into stage nit & 1 (whole waves skip a partial last one).
+    auto issue_all = [&]() {
+        float* st = smem + (nit & 1) * STAGE;
+#pragma unroll
+        for (int i = 0; i < NL; ++i) {
+            const int ii = i < LA ? i : i - LA;
+            const int total_ch = i < LA ? A_CH : W_CH;
+            if (total_ch % NT == 0 || ii * NT + wave * 64 < total_ch)
+                load_lds16_async(src[i], st + (i < LA ? 0 : BM * BK) + (ii * NT + wave * 64) * 4);
+        }
+    };
+    auto advance = [&]() {
+        ++nit;
+        if (nit < total) {
+            if (nit - (nit / nk) * nk == 0) {
+                point_at(nit);
+            } else {
+#pragma unroll
+                for (int i = 0; i < NL; ++i) src[i] += BK;
+            }
+        }
+    };
+
+    const int sw = chunk_swizzle16<CPR>(l32);
+    const int a_row = (wm * WM + l32) * BK, w_row = BM * BK + (wn * WN + l32) * BK;
+
+    // Epilogue lane map: pass qq of block row i covers wave-tile rows
+    // i*32 + qq*RPP + lane / C4, columns 4 * (lane % C4) .. +3, so every global
+    // access is a row-contiguous float4.
+    const int e_r = lane / C4, e_c = 4 * (lane % C4);
+
+    point_at(0);
+    issue_all();
+    advance();
+    int it = 0;
+    for (int t = 0; t < my_tiles; ++t) {
+        const int tile = wg + t * G;
+        const int m0 = (tile / ntiles_n) * BM, n0 = (tile - (tile / ntiles_n) * ntiles_n) * BN;
+        v16f acc[FM][FN];
+#pragma unroll
+        for (int i = 0; i < FM; ++i)
+#pragma unroll
+            for (int j = 0; j < FN; ++j)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+        for (int kt = 0; kt < nk; ++kt, ++it) {
+            wait_all_then_barrier();
+            if (it + 1 < total) issue_all();
+            const float* st = smem + (it & 1) * STAGE;
+#pragma unroll
+            for (int s = 0; s < KS; ++s) {
+                const int ko = 4 * ((2 * s + half) ^ sw);
+                v4f af[FM], wf[FN];
+#pragma unroll
+                for (int i = 0; i < FM; ++i)
+                    af[i] = *reinterpret_cast<const v4f*>(st + a_row + i * 32 * BK + ko);
+#pragma unroll
+                for (int j = 0; j < FN; ++j)
+                    wf[j] = *reinterpret_cast<const v4f*>(st + w_row + j * 32 * BK + ko);
+#pragma unroll
+                for (int q = 0; q < 4; ++q)
+#pragma unroll
+                    for (int i = 0; i < FM; ++i)
+#pragma unroll
+                        for (int j = 0; j < FN; ++j)
+                            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(af[i][q], wf[j][q],
+                                                                             acc[i][j], 0, 0, 0);
+            }
+            if (it + 1 < total) advance();
+        }
+
+        // ---- epilogue: bias (+ GELU | + residual), through LDS as float4 rows ----
+        const int gc = n0 + wn * WN + e_c;                      // first of this lane's 4 columns
+        const bool col_ok = gc < N;                             // N % 4 == 0: all 4 or none
+        const int grow0 = m0 + wm * WM + e_r;
+        float4 bias4 = col_ok ? *reinterpret_cast<const float4*>(p.bias + gc) : make_float4(0, 0, 0, 0);
+        float4 res[NP];
+        if constexpr (EPI == EPI_BIAS_RESID) {
+#pragma unroll
+            for (int q = 0; q < NP; ++q) {
+                const int row = min(grow0 + (q / NPB) * 32 + (q % NPB) * RPP, M - 1);
+                res[q] = col_ok ? *reinterpret_cast<const float4*>(p.R + (int64_t)row * p.ldr + gc)
+                                : make_float4(0, 0, 0, 0);
+            }
+        }
+        // Every wave has finished reading this stage's fragments: reuse it for C,
+        // 32 rows (one MFMA block row) of this wave's tile at a time.
+        wait_lds_then_barrier();
+        float* cw = smem + ((it - 1) & 1) * STAGE + wave * (32 * WN);
+#pragma unroll
+        for (int i = 0; i < FM; ++i) {
+#pragma unroll
+            for (int j = 0; j < FN; ++j)
+#pragma unroll
+                for (int r = 0; r < 16; ++r)
+                    cw[(8 * (r >> 2) + 4 * half + (r & 3)) * WN + j * 32 + l32] = acc[i][j][r];
+#pragma unroll
+            for (int qq = 0; qq < NPB; ++qq) {
+                const int q = i * NPB + qq;
+                float4 v = *reinterpret_cast<const float4*>(cw + (qq * RPP + e_r) * WN + e_c);
+                v.x += bias4.x; v.y += bias4.y; v.z += bias4.z; v.w += bias4.w;
+                if constexpr (EPI == EPI_BIAS_GELU) {
+                    v.x = gelu_tanh_fast(v.x); v.y = gelu_tanh_fast(v.y);
+                    v.z = gelu_tanh_fast(v.z); v.w = gelu_tanh_fast(v.w);
+                }
+                if constexpr (EPI == EPI_BIAS_RESID) {
+                    v.x += res[q].x; v.y += res[q].y; v.z += res[q].z; v.w += res[q].w;
+                }
+                const int row = grow0 + i * 32 + qq * RPP;
+                if (col_ok && row < M) *reinterpret_cast<float4*>(p.C + (int64_t)row * p.ldc + gc) = v;
             }
         }
     }
@@ -322,20 +728,20 @@ __global__ __launch_bounds__(256) void gemm_bf16_kernel(GemmArgs p) {
 // ---------------------------------------------------------------------------
 // launchers
 // ---------------------------------------------------------------------------
-template <int BM, int BN, int BK, int WAVES_M, int WAVES_N, bool BF16>
+template <int BM, int BN, int BK, int WAVES_M, int WAVES_N, bool BF16, bool KFULL = false>
 static hipError_t launch_tile(const GemmArgs& a, int epi, hipStream_t s) {
     const int mt = (a.M_max + BM - 1) / BM, nt = (a.N + BN - 1) / BN;
-    const dim3 grid(mt * nt), block(256);
+    const dim3 grid(mt * nt), block(64 * WAVES_M * WAVES_N);
     if (mt == 0 || nt == 0) return hipSuccess;
     switch (epi) {
 #define EBH_CASE(E)                                                                           \
     case E:                                                                                   \
-        if (BF16)                                                                             \
+        if constexpr (BF16)                                                                   \
             hipLaunchKernelGGL((gemm_bf16_kernel<BM, BN, BK, WAVES_M, WAVES_N, E>), grid,     \
                                block, 0, s, a);                                               \
         else                                                                                  \
-            hipLaunchKernelGGL((gemm_f32_kernel<BM, BN, BK, WAVES_M, WAVES_N, E>), grid,      \
-                               block, 0, s, a);                                               \
+            hipLaunchKernelGGL((gemm_f32_kernel<BM, BN, BK, WAVES_M, WAVES_N, E, KFULL>),     \
+                               grid, block, 0, s, a);                                         \
         break;
         EBH_CASE(EPI_BIAS)
         EBH_CASE(EPI_BIAS_GELU)
@@ -347,7 +753,84 @@ static hipError_t launch_tile(const GemmArgs& a, int epi, hipStream_t s) {
     return hipGetLastError();
 }
 
+template <int BM, int BN, int BK, int WAVES_M, int WAVES_N>
+static hipError_t launch_dtl(const GemmArgs& a, int epi, hipStream_t s) {
+    const int mt = (a.M_max + BM - 1) / BM, nt = (a.N + BN - 1) / BN;
+    const dim3 grid(mt * nt), block(64 * WAVES_M * WAVES_N);
+    if (mt == 0 || nt == 0) return hipSuccess;
+    switch (epi) {
+        case EPI_BIAS:
+            hipLaunchKernelGGL((gemm_f32_dtl_kernel<BM, BN, BK, WAVES_M, WAVES_N, EPI_BIAS>), grid, block, 0, s, a);
+            break;
+        case EPI_BIAS_GELU:
+            hipLaunchKernelGGL((gemm_f32_dtl_kernel<BM, BN, BK, WAVES_M, WAVES_N, EPI_BIAS_GELU>), grid, block, 0, s, a);
+            break;
+        case EPI_BIAS_RESID:
+            hipLaunchKernelGGL((gemm_f32_dtl_kernel<BM, BN, BK, WAVES_M, WAVES_N, EPI_BIAS_RESID>), grid, block, 0, s, a);
+            break;
+        default:
+            return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+// Persistent launch: min(tiles, CUs) workgroups (one per CU: the two LDS
+// stages take 128 KB at BK = 64).
+static int cu_count() {
+    static int n = 0;
+    if (n == 0) {
+        int dev = 0, v = 0;
+        if (hipGetDevice(&dev) == hipSuccess &&
+            hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && v > 0)
+            n = v;
+        else
+            n = 256;
+    }
+    return n;
+}
+
+template <int BM, int BN, int BK, int WAVES_M, int WAVES_N>
+static hipError_t launch_persistent(const GemmArgs& a, int epi, hipStream_t s, int wg_per_cu = 1) {
+    const int64_t tiles = (int64_t)((a.M_max + BM - 1) / BM) * ((a.N + BN - 1) / BN);
+    if (tiles == 0) return hipSuccess;
+    const int grid = (int)std::min<int64_t>(tiles, (int64_t)cu_count() * wg_per_cu);
+    const dim3 block(64 * WAVES_M * WAVES_N);
+    switch (epi) {
+        case EPI_BIAS:
+            hipLaunchKernelGGL((gemm_f32_persistent_kernel<BM, BN, BK, WAVES_M, WAVES_N, EPI_BIAS>), dim3(grid), block, 0, s, a);
+            break;
+        case EPI_BIAS_GELU:
+            hipLaunchKernelGGL((gemm_f32_persistent_kernel<BM, BN, BK, WAVES_M, WAVES_N, EPI_BIAS_GELU>), dim3(grid), block, 0, s, a);
+            break;
+        case EPI_BIAS_RESID:
+            hipLaunchKernelGGL((gemm_f32_persistent_kernel<BM, BN, BK, WAVES_M, WAVES_N, EPI_BIAS_RESID>), dim3(grid), block, 0, s, a);
+            break;
+        default:
+            return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+static bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
+
+// fp32 dispatch.  The persistent kernels need 16-byte aligned rows and
+// operands, N % 4 == 0 (float4 epilogue) and K a multiple of their k-tile;
+// anything else takes the guarded register-staged kernel.  Tile choice (c3
+// shapes, MI355X): a 64-deep k-tile with 8 waves for the K = 384 projections,
+// 4 waves for long K (FFN down), and 32-deep with two workgroups per CU for
+// wide outputs (FFN up), where one workgroup's epilogue overlaps the other's MFMAs.
 hipError_t launch_gemm_f32(const GemmArgs& a, int epi, hipStream_t s) {
+    const bool aligned = aligned16(a.A) && aligned16(a.W) && aligned16(a.C) && aligned16(a.bias) &&
+                         (epi != EPI_BIAS_RESID || (aligned16(a.R) && a.ldr % 4 == 0)) &&
+                         a.lda % 4 == 0 && a.ldw % 4 == 0 && a.ldc % 4 == 0 && a.N % 4 == 0;
+    if (aligned && a.K % 64 == 0 && a.K >= 1024)
+        return launch_persistent<128, 128, 64, 2, 2>(a, epi, s, 1);
+    if (aligned && a.K % 32 == 0 && a.N >= 1536)
+        return launch_persistent<128, 128, 32, 2, 4>(a, epi, s, 2);
+    if (aligned && a.K % 64 == 0)
+        return launch_persistent<128, 128, 64, 2, 4>(a, epi, s, 1);
+    if (aligned && a.K % 32 == 0)
+        return launch_persistent<128, 128, 32, 2, 4>(a, epi, s, 2);
     return launch_tile<128, 128, 32, 2, 2, false>(a, epi, s);
 }
 
