@@ -22,7 +22,7 @@ EBH_ERR_HIP = -5
 EBH_ERR_RANGE = -6
 EBH_DTYPE_F32 = 0
 EBH_DTYPE_BF16 = 1
-EPI_BIAS, EPI_BIAS_GELU, EPI_BIAS_RESID = 0, 1, 2
+EPI_BIAS, EPI_BIAS_GELU, EPI_BIAS_RESID, EPI_NONE = 0, 1, 2, 3
 PROF = {"none": 0, "gemm_qkv": 1, "attention": 2, "gemm_out": 3, "gemm_ffn_up": 4,
         "gemm_ffn_down": 5, "layernorm": 6, "embed": 7, "pool": 8}
 
@@ -65,6 +65,7 @@ _SIGS = {
                            _i32, _i32, _vp]),
     "ebh_op_attention": (_i32, [_vp, _vp, _i32, _i32, _i32, _i32, _vp, _vp]),
     "ebh_op_layer_norm": (_i32, [_vp, _vp, _vp, _i32, _i32, _f32, _vp, _vp]),
+    "ebh_op_add_layer_norm": (_i32, [_vp, _vp, _vp, _vp, _vp, _i32, _i32, _f32, _vp]),
     "ebh_op_pool": (_i32, [_vp, _vp, _i32, _i32, _i32, _i32, _vp, _vp]),
     "ebh_op_pack": (_i32, [_vp, _vp, _i32, _i32, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
     "ebh_op_embed_ln": (_i32, [_vp, _vp, _vp, _i32, _vp, _vp, _vp, _vp, _vp, _i32, _i32, _f32,

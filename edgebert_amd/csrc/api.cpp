@@ -306,6 +306,9 @@ int enqueue_forward(ebh_model* m, const int* d_ids, const int* d_mask, int B, in
         return EBH_OK;
     };
 
+    // Per layer (BertLayer::forward, src/lib.rs:669-683): the attention-output and
+    // FFN-down projections are written without bias; their bias and the block's
+    // residual are added, in the reference's order, by the LayerNorm that follows.
     for (const DevLayer& L : m->layers) {
         int rc;
         if ((rc = gemm(EBH_PROF_GEMM_QKV, w.X, L.wqkv, L.wqkv16, L.bqkv, nullptr, w.QKV, 3 * H, H,
@@ -314,20 +317,20 @@ int enqueue_forward(ebh_model* m, const int* d_ids, const int* d_mask, int B, in
         prof_begin(m, EBH_PROF_ATTENTION, s, pp, on);
         HIP_TRY(ebh::launch_attention(w.QKV, w.cu, B, S, H, nh, hd, scale, w.CTX, s));
         prof_end(m, s, pp, on);
-        if ((rc = gemm(EBH_PROF_GEMM_OUT, w.CTX, L.wo, L.wo16, L.bo, w.X, w.Y, H, H,
-                       ebh::EPI_BIAS_RESID)))
+        if ((rc = gemm(EBH_PROF_GEMM_OUT, w.CTX, L.wo, L.wo16, nullptr, nullptr, w.Y, H, H,
+                       ebh::EPI_NONE)))
             return rc;
         prof_begin(m, EBH_PROF_LAYERNORM, s, pp, on);
-        HIP_TRY(ebh::launch_layernorm(w.Y, w.X, L.ln1_g, L.ln1_b, T, w.ntok, H, eps, s));
+        HIP_TRY(ebh::launch_add_layernorm(w.Y, L.bo, w.X, L.ln1_g, L.ln1_b, T, w.ntok, H, eps, s));
         prof_end(m, s, pp, on);
         if ((rc = gemm(EBH_PROF_GEMM_FFN_UP, w.X, L.w1, L.w116, L.b1, nullptr, w.F, I, H,
                        ebh::EPI_BIAS_GELU)))
             return rc;
-        if ((rc = gemm(EBH_PROF_GEMM_FFN_DOWN, w.F, L.w2, L.w216, L.b2, w.X, w.Y, H, I,
-                       ebh::EPI_BIAS_RESID)))
+        if ((rc = gemm(EBH_PROF_GEMM_FFN_DOWN, w.F, L.w2, L.w216, nullptr, nullptr, w.Y, H, I,
+                       ebh::EPI_NONE)))
             return rc;
         prof_begin(m, EBH_PROF_LAYERNORM, s, pp, on);
-        HIP_TRY(ebh::launch_layernorm(w.Y, w.X, L.ln2_g, L.ln2_b, T, w.ntok, H, eps, s));
+        HIP_TRY(ebh::launch_add_layernorm(w.Y, L.b2, w.X, L.ln2_g, L.ln2_b, T, w.ntok, H, eps, s));
         prof_end(m, s, pp, on);
     }
     prof_begin(m, EBH_PROF_POOL, s, pp, on);
@@ -706,9 +709,10 @@ int ebh_profile_read(ebh_model* m, int64_t* launches, double* total_ms) {
 int ebh_op_gemm(const float* A, int64_t lda, const void* W, int64_t ldw, int32_t w_dtype,
                 const float* bias, const float* residual, int64_t ldr, float* C, int64_t ldc,
                 int32_t M, int32_t N, int32_t K, int32_t epilogue, void* stream) {
-    if (!A || !W || !bias || !C) return fail(EBH_ERR_INVALID_ARG, "null buffer");
+    if (!A || !W || !C || (!bias && epilogue != EBH_EPI_NONE))
+        return fail(EBH_ERR_INVALID_ARG, "null buffer");
     if (M < 0 || N <= 0 || K <= 0) return fail(EBH_ERR_INVALID_ARG, "bad GEMM shape");
-    if (epilogue < EBH_EPI_BIAS || epilogue > EBH_EPI_BIAS_RESID)
+    if (epilogue < EBH_EPI_BIAS || epilogue > EBH_EPI_NONE)
         return fail(EBH_ERR_INVALID_ARG, "unknown epilogue %d", epilogue);
     if (epilogue == EBH_EPI_BIAS_RESID && (!residual || ldr < N))
         return fail(EBH_ERR_INVALID_ARG, "residual epilogue needs a residual of row stride >= N");
@@ -748,6 +752,15 @@ int ebh_op_layer_norm(const float* x, const float* gamma, const float* beta, int
     if (rows < 0 || H <= 0 || H > 2048) return fail(EBH_ERR_INVALID_ARG, "bad LayerNorm shape");
     HIP_TRY(ebh::launch_layernorm(x, y, gamma, beta, rows, nullptr, H, eps,
                                   static_cast<hipStream_t>(stream)));
+    return EBH_OK;
+}
+
+int ebh_op_add_layer_norm(const float* y, const float* bias, float* x, const float* gamma,
+                          const float* beta, int32_t rows, int32_t H, float eps, void* stream) {
+    if (!y || !bias || !x || !gamma || !beta) return fail(EBH_ERR_INVALID_ARG, "null buffer");
+    if (rows < 0 || H <= 0 || H > 2048) return fail(EBH_ERR_INVALID_ARG, "bad LayerNorm shape");
+    HIP_TRY(ebh::launch_add_layernorm(y, bias, x, gamma, beta, rows, nullptr, H, eps,
+                                      static_cast<hipStream_t>(stream)));
     return EBH_OK;
 }
 

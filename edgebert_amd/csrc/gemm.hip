@@ -43,7 +43,7 @@ __device__ __forceinline__ void tile_coords(int ntiles_n, int& mt, int& nt) {
 template <int EPI>
 __device__ __forceinline__ float epilogue(float acc, float bias, const float* R, int64_t ldr,
                                           int row, int col) {
-    float v = acc + bias;
+    float v = EPI == EPI_NONE ? acc : acc + bias;
     if (EPI == EPI_BIAS_GELU) v = gelu_tanh(v);
     if (EPI == EPI_BIAS_RESID) v = v + R[(int64_t)row * ldr + col];
     return v;
@@ -353,19 +353,27 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_f32_dtl_kernel(Ge
 }
 
 // ---------------------------------------------------------------------------
-// fp32, persistent: one workgroup per CU walks a strided list of 128x128 C
-// tiles, flattening (tile, k-tile) into one pipelined loop, so the next tile's
-// first loads overlap the current tile's last MFMAs and epilogue.
+// fp32, persistent: one workgroup per CU walks a strided list of BM x BN C
+// tiles through one flattened (tile, k-tile) pipeline with NSTAGE LDS stages,
+// so the loads of the next NSTAGE-1 k-tiles (across tile boundaries) are in
+// flight while the MFMAs of the current one run.
 //
-// Loads use global_load_lds_dwordx4 issued from inline asm: the compiler's
-// wait-count tracking does not see them, so it does not force every LDS read
-// to wait for every outstanding LDS load; the loop waits explicitly instead
-// (vmcnt(0) + barrier at the top of each k-tile).  That lets a wave read the
-// fragments of k-slice s+1 while the MFMAs of slice s run.  M0 (the LDS
-// destination base of the instruction) is saved and restored inside the asm.
+// Loads are global_load_lds_dwordx4 issued from inline asm: the compiler's
+// wait-count tracking does not see them, so it does not make every LDS read
+// wait for every outstanding LDS load.  The loop waits explicitly instead:
+// before k-tile `it` is used, vmcnt(n) with n = the load instructions this
+// wave issued after k-tile it's own (every wave issues the same number, and
+// vector memory operations complete in issue order), then the barrier.
+// M0 (the LDS destination base of the instruction) is saved and restored
+// inside the asm.  The bias row segment of a tile comes the same way, into a
+// small per-wave LDS slot, so the epilogue issues no global load.
 //
-// LDS: two stages of [BM][BK] + [BN][BK] floats, 16-byte chunks XOR-swizzled
-// within each row (conflict-free fragment reads, see chunk_swizzle).
+// A tile's epilogue runs at the top of the next tile's first k-tile, after
+// that k-tile's wait and before its loads are issued: the C tile is
+// transposed through the LDS stage the previous k-tile used (free until the
+// loads issued right after the epilogue refill it) and written as
+// row-contiguous float4.  Its stores are then older than every load still to
+// be waited for, so no later wait depends on them finishing early.
 // ---------------------------------------------------------------------------
 __device__ __forceinline__ void load_lds16_async(const float* g, const float* lds) {
     const uint32_t base = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)lds);
@@ -381,22 +389,31 @@ __device__ __forceinline__ void load_lds16_async(const float* g, const float* ld
         : "memory");
 }
 
-// Every load this wave issued has landed in LDS and every LDS read has
-// returned; then the workgroup barrier.
-__device__ __forceinline__ void wait_all_then_barrier() {
-    asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+// At most n vector-memory operations of this wave outstanding (n is
+// wave-uniform; s_waitcnt takes an immediate, so switch over the small range
+// the pipelines use; larger n waits for everything, which is always safe).
+__device__ __forceinline__ void wait_vmcnt(int n) {
+    switch (n) {
+#define EBH_VMCNT(k) \
+    case k: asm volatile("s_waitcnt vmcnt(" #k ")" ::: "memory"); break;
+        EBH_VMCNT(1) EBH_VMCNT(2) EBH_VMCNT(3) EBH_VMCNT(4) EBH_VMCNT(5) EBH_VMCNT(6)
+        EBH_VMCNT(7) EBH_VMCNT(8) EBH_VMCNT(9) EBH_VMCNT(10) EBH_VMCNT(11) EBH_VMCNT(12)
+        EBH_VMCNT(13) EBH_VMCNT(14) EBH_VMCNT(15) EBH_VMCNT(16) EBH_VMCNT(17) EBH_VMCNT(18)
+        EBH_VMCNT(19) EBH_VMCNT(20) EBH_VMCNT(21) EBH_VMCNT(22) EBH_VMCNT(23) EBH_VMCNT(24)
+#undef EBH_VMCNT
+        default: asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); break;
+    }
+}
+
+// This wave's LDS reads have returned; then the workgroup barrier.
+__device__ __forceinline__ void lds_barrier() {
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 }
 
 template <int CPR>
 __device__ __forceinline__ int chunk_swizzle16(int r) {
     if constexpr (CPR == 16) return r & 15;
     else return chunk_swizzle<CPR>(r);
-}
-
-// Only LDS reads / writes of this wave are outstanding, then the barrier (the
-// next k-tile's loads may still be landing in the other stage).
-__device__ __forceinline__ void wait_lds_then_barrier() {
-    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 }
 
 // tanh-form GELU of the reference (constants of src/lib.rs:151-152) with
@@ -411,27 +428,29 @@ __device__ __forceinline__ float gelu_tanh_fast(float val) {
     return val * 0.5f * (1.0f + t);
 }
 
-template <int BM, int BN, int BK, int WAVES_M, int WAVES_N, int EPI>
+template <int BM, int BN, int BK, int WAVES_M, int WAVES_N, int NSTAGE, int EPI>
 __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_f32_persistent_kernel(GemmArgs p) {
-    constexpr int NT = 64 * WAVES_M * WAVES_N;
+    static_assert(EPI == EPI_BIAS || EPI == EPI_BIAS_GELU || EPI == EPI_NONE, "no residual here");
+    constexpr bool HAS_BIAS = EPI != EPI_NONE;
+    constexpr int NT = 64 * WAVES_M * WAVES_N, NW = WAVES_M * WAVES_N;
     constexpr int WM = BM / WAVES_M, WN = BN / WAVES_N;
     constexpr int FM = WM / 32, FN = WN / 32;
     static_assert(FM * 32 == WM && FN * 32 == WN, "wave tile must be whole 32x32 blocks");
     constexpr int CPR = BK / 4;                   // 16-byte chunks per tile row
     constexpr int KS = BK / 8;                    // 8-wide k slices per k-tile
     constexpr int A_CH = BM * CPR, W_CH = BN * CPR;
-    constexpr int LA = (A_CH + NT - 1) / NT, LW = (W_CH + NT - 1) / NT;
-    static_assert(A_CH % 64 == 0 && W_CH % 64 == 0, "a load instruction fills 64 chunks per wave");
-    constexpr int STAGE = (BM + BN) * BK;         // floats per LDS stage: A rows, then W rows
-    constexpr int NW = WAVES_M * WAVES_N;
+    static_assert(A_CH % NT == 0 && W_CH % NT == 0, "every wave issues the same loads");
+    constexpr int LA = A_CH / NT, LW = W_CH / NT, NL = LA + LW;
+    constexpr int D = NSTAGE - 1;                 // k-tiles in flight ahead
+    constexpr int STAGE = (BM + BN) * BK;         // floats per stage: A rows, then W rows
     static_assert(NW * 32 * WN <= STAGE, "each wave transposes 32 C rows at a time through one stage");
     constexpr int C4 = WN / 4;                    // float4 per wave-tile row
     constexpr int RPP = 64 / C4;                  // wave-tile rows per float4 pass
     static_assert(C4 * RPP == 64 && 32 % RPP == 0, "epilogue pass shape");
     constexpr int NPB = 32 / RPP;                 // float4 passes per 32-row block
-    constexpr int NP = FM * NPB;                  // float4 passes per lane
+    constexpr int BIAS_SLOT = 256;                // floats: one wave's 64 x 16-byte bias chunks
 
-    __shared__ __attribute__((aligned(16))) float smem[2 * STAGE];
+    __shared__ __attribute__((aligned(16))) float smem[NSTAGE * STAGE + (HAS_BIAS ? 2 * NW * BIAS_SLOT : 0)];
 
     const int M = p.M_dev ? *p.M_dev : p.M_max;
     const int N = p.N;
@@ -453,7 +472,6 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_f32_persistent_ke
     const float* __restrict__ W = static_cast<const float*>(p.W);
 
     // This lane's share of each k-tile load: row and swizzled k-chunk of LDS chunk i*NT + tid.
-    constexpr int NL = LA + LW;                   // load instructions per k-tile
     int l_r[NL], l_c[NL];
 #pragma unroll
     for (int i = 0; i < NL; ++i) {
@@ -464,6 +482,7 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_f32_persistent_ke
     // Source pointers of the next k-tile to load (iteration `nit`), advanced by BK
     // per k-tile and recomputed when that k-tile starts a new C tile.
     const float* src[NL];
+    const float* bias_src = nullptr;
     int nit = 0;
     auto point_at = [&](int it) {
         const int t = wg + (it / nk) * G, kt = it - (it / nk) * nk;
@@ -472,22 +491,20 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_f32_persistent_ke
         for (int i = 0; i < NL; ++i)
             src[i] = i < LA ? A + (int64_t)min(m0 + l_r[i], M - 1) * p.lda + kt * BK + l_c[i]
                             : W + (int64_t)min(n0 + l_r[i], N - 1) * p.ldw + kt * BK + l_c[i];
+        if (HAS_BIAS) bias_src = p.bias + min(n0 + wn * WN + 4 * lane, N - 4);
     };
-    // Every load of k-tile `nit` into stage nit & 1 (whole waves skip a partial last one).
-    auto issue_all = [&]() {
-        float* st = smem + (nit & 1) * STAGE;
+    // Load instructions of k-tile j (the bias chunk rides with a tile's first k-tile).
+    auto n_issued = [&](int j) { return NL + (HAS_BIAS && j % nk == 0 ? 1 : 0); };
+    auto issue = [&]() {
+        float* st = smem + (nit % NSTAGE) * STAGE;
 #pragma unroll
-        for (int i = 0; i < NL; ++i) {
-            const int ii = i < LA ? i : i - LA;
-            const int total_ch = i < LA ? A_CH : W_CH;
-            if (total_ch % NT == 0 || ii * NT + wave * 64 < total_ch)
-                load_lds16_async(src[i], st + (i < LA ? 0 : BM * BK) + (ii * NT + wave * 64) * 4);
-        }
-    };
-    auto advance = [&]() {
+        for (int i = 0; i < NL; ++i)
+            load_lds16_async(src[i], st + (i < LA ? 0 : BM * BK) + ((i < LA ? i : i - LA) * NT + wave * 64) * 4);
+        if (HAS_BIAS && nit % nk == 0)
+            load_lds16_async(bias_src, smem + NSTAGE * STAGE + (((nit / nk) & 1) * NW + wave) * BIAS_SLOT);
         ++nit;
         if (nit < total) {
-            if (nit - (nit / nk) * nk == 0) {
+            if (nit % nk == 0) {
                 point_at(nit);
             } else {
 #pragma unroll
@@ -498,30 +515,69 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_f32_persistent_ke
 
     const int sw = chunk_swizzle16<CPR>(l32);
     const int a_row = (wm * WM + l32) * BK, w_row = BM * BK + (wn * WN + l32) * BK;
-
     // Epilogue lane map: pass qq of block row i covers wave-tile rows
-    // i*32 + qq*RPP + lane / C4, columns 4 * (lane % C4) .. +3, so every global
-    // access is a row-contiguous float4.
+    // i*32 + qq*RPP + lane / C4, columns 4 * (lane % C4) .. +3.
     const int e_r = lane / C4, e_c = 4 * (lane % C4);
 
-    point_at(0);
-    issue_all();
-    advance();
-    int it = 0;
-    for (int t = 0; t < my_tiles; ++t) {
+    v16f acc[FM][FN];
+    // Epilogue of local tile t: bias (+ GELU), C through LDS stage `cs`, float4 stores.
+    auto epilogue_tile = [&](int t, const float* cs_base) {
         const int tile = wg + t * G;
         const int m0 = (tile / ntiles_n) * BM, n0 = (tile - (tile / ntiles_n) * ntiles_n) * BN;
-        v16f acc[FM][FN];
+        const int gc = n0 + wn * WN + e_c;
+        const bool col_ok = gc < N;  // N % 4 == 0: all 4 columns or none
+        float4 bias4 = make_float4(0, 0, 0, 0);
+        if (HAS_BIAS)
+            bias4 = *reinterpret_cast<const float4*>(smem + NSTAGE * STAGE + ((t & 1) * NW + wave) * BIAS_SLOT + e_c);
+        float* cw = const_cast<float*>(cs_base) + wave * (32 * WN);
+        const int grow0 = m0 + wm * WM + e_r;
 #pragma unroll
-        for (int i = 0; i < FM; ++i)
+        for (int i = 0; i < FM; ++i) {
 #pragma unroll
             for (int j = 0; j < FN; ++j)
 #pragma unroll
-                for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+                for (int r = 0; r < 16; ++r)
+                    cw[(8 * (r >> 2) + 4 * half + (r & 3)) * WN + j * 32 + l32] = acc[i][j][r];
+#pragma unroll
+            for (int qq = 0; qq < NPB; ++qq) {
+                float4 v = *reinterpret_cast<const float4*>(cw + (qq * RPP + e_r) * WN + e_c);
+                if (HAS_BIAS) { v.x += bias4.x; v.y += bias4.y; v.z += bias4.z; v.w += bias4.w; }
+                if constexpr (EPI == EPI_BIAS_GELU) {
+                    v.x = gelu_tanh_fast(v.x); v.y = gelu_tanh_fast(v.y);
+                    v.z = gelu_tanh_fast(v.z); v.w = gelu_tanh_fast(v.w);
+                }
+                const int row = grow0 + i * 32 + qq * RPP;
+                if (col_ok && row < M) *reinterpret_cast<float4*>(p.C + (int64_t)row * p.ldc + gc) = v;
+            }
+        }
+    };
+
+    point_at(0);
+#pragma unroll
+    for (int d = 0; d < D; ++d)
+        if (nit < total) issue();
+    int it = 0;
+    for (int t = 0; t < my_tiles; ++t) {
         for (int kt = 0; kt < nk; ++kt, ++it) {
-            wait_all_then_barrier();
-            if (it + 1 < total) issue_all();
-            const float* st = smem + (it & 1) * STAGE;
+            // k-tile `it` has landed once only the loads issued after it remain.
+            int after = 0;
+            for (int j = it + 1; j < nit; ++j) after += n_issued(j);
+            wait_vmcnt(after);
+            lds_barrier();
+            if (kt == 0) {
+                if (t > 0) {
+                    epilogue_tile(t - 1, smem + ((it - 1) % NSTAGE) * STAGE);
+                    lds_barrier();  // the stage is refilled by the loads below
+                }
+#pragma unroll
+                for (int i = 0; i < FM; ++i)
+#pragma unroll
+                    for (int j = 0; j < FN; ++j)
+#pragma unroll
+                        for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+            }
+            if (nit < total) issue();
+            const float* st = smem + (it % NSTAGE) * STAGE;
 #pragma unroll
             for (int s = 0; s < KS; ++s) {
                 const int ko = 4 * ((2 * s + half) ^ sw);
@@ -541,51 +597,10 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_f32_persistent_ke
                             acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(af[i][q], wf[j][q],
                                                                              acc[i][j], 0, 0, 0);
             }
-            if (it + 1 < total) advance();
-        }
-
-        // ---- epilogue: bias (+ GELU | + residual), through LDS as float4 rows ----
-        const int gc = n0 + wn * WN + e_c;                      // first of this lane's 4 columns
-        const bool col_ok = gc < N;                             // N % 4 == 0: all 4 or none
-        const int grow0 = m0 + wm * WM + e_r;
-        float4 bias4 = col_ok ? *reinterpret_cast<const float4*>(p.bias + gc) : make_float4(0, 0, 0, 0);
-        float4 res[NP];
-        if constexpr (EPI == EPI_BIAS_RESID) {
-#pragma unroll
-            for (int q = 0; q < NP; ++q) {
-                const int row = min(grow0 + (q / NPB) * 32 + (q % NPB) * RPP, M - 1);
-                res[q] = col_ok ? *reinterpret_cast<const float4*>(p.R + (int64_t)row * p.ldr + gc)
-                                : make_float4(0, 0, 0, 0);
-            }
-        }
-        // Every wave has finished reading this stage's fragments: reuse it for C,
-        // 32 rows (one MFMA block row) of this wave's tile at a time.
-        wait_lds_then_barrier();
-        float* cw = smem + ((it - 1) & 1) * STAGE + wave * (32 * WN);
-#pragma unroll
-        for (int i = 0; i < FM; ++i) {
-#pragma unroll
-            for (int j = 0; j < FN; ++j)
-#pragma unroll
-                for (int r = 0; r < 16; ++r)
-                    cw[(8 * (r >> 2) + 4 * half + (r & 3)) * WN + j * 32 + l32] = acc[i][j][r];
-#pragma unroll
-            for (int qq = 0; qq < NPB; ++qq) {
-                const int q = i * NPB + qq;
-                float4 v = *reinterpret_cast<const float4*>(cw + (qq * RPP + e_r) * WN + e_c);
-                v.x += bias4.x; v.y += bias4.y; v.z += bias4.z; v.w += bias4.w;
-                if constexpr (EPI == EPI_BIAS_GELU) {
-                    v.x = gelu_tanh_fast(v.x); v.y = gelu_tanh_fast(v.y);
-                    v.z = gelu_tanh_fast(v.z); v.w = gelu_tanh_fast(v.w);
-                }
-                if constexpr (EPI == EPI_BIAS_RESID) {
-                    v.x += res[q].x; v.y += res[q].y; v.z += res[q].z; v.w += res[q].w;
-                }
-                const int row = grow0 + i * 32 + qq * RPP;
-                if (col_ok && row < M) *reinterpret_cast<float4*>(p.C + (int64_t)row * p.ldc + gc) = v;
-            }
         }
     }
+    lds_barrier();  // every wave is done with the last k-tile's stage
+    epilogue_tile(my_tiles - 1, smem + ((it - 1) % NSTAGE) * STAGE);
 }
 
 // ---------------------------------------------------------------------------
@@ -746,6 +761,7 @@ static hipError_t launch_tile(const GemmArgs& a, int epi, hipStream_t s) {
         EBH_CASE(EPI_BIAS)
         EBH_CASE(EPI_BIAS_GELU)
         EBH_CASE(EPI_BIAS_RESID)
+        EBH_CASE(EPI_NONE)
 #undef EBH_CASE
         default:
             return hipErrorInvalidValue;
@@ -768,6 +784,9 @@ static hipError_t launch_dtl(const GemmArgs& a, int epi, hipStream_t s) {
         case EPI_BIAS_RESID:
             hipLaunchKernelGGL((gemm_f32_dtl_kernel<BM, BN, BK, WAVES_M, WAVES_N, EPI_BIAS_RESID>), grid, block, 0, s, a);
             break;
+        case EPI_NONE:
+            hipLaunchKernelGGL((gemm_f32_dtl_kernel<BM, BN, BK, WAVES_M, WAVES_N, EPI_NONE>), grid, block, 0, s, a);
+            break;
         default:
             return hipErrorInvalidValue;
     }
@@ -789,7 +808,7 @@ static int cu_count() {
     return n;
 }
 
-template <int BM, int BN, int BK, int WAVES_M, int WAVES_N>
+template <int BM, int BN, int BK, int WAVES_M, int WAVES_N, int NSTAGE>
 static hipError_t launch_persistent(const GemmArgs& a, int epi, hipStream_t s, int wg_per_cu = 1) {
     const int64_t tiles = (int64_t)((a.M_max + BM - 1) / BM) * ((a.N + BN - 1) / BN);
     if (tiles == 0) return hipSuccess;
@@ -797,13 +816,13 @@ static hipError_t launch_persistent(const GemmArgs& a, int epi, hipStream_t s, i
     const dim3 block(64 * WAVES_M * WAVES_N);
     switch (epi) {
         case EPI_BIAS:
-            hipLaunchKernelGGL((gemm_f32_persistent_kernel<BM, BN, BK, WAVES_M, WAVES_N, EPI_BIAS>), dim3(grid), block, 0, s, a);
+            hipLaunchKernelGGL((gemm_f32_persistent_kernel<BM, BN, BK, WAVES_M, WAVES_N, NSTAGE, EPI_BIAS>), dim3(grid), block, 0, s, a);
             break;
         case EPI_BIAS_GELU:
-            hipLaunchKernelGGL((gemm_f32_persistent_kernel<BM, BN, BK, WAVES_M, WAVES_N, EPI_BIAS_GELU>), dim3(grid), block, 0, s, a);
+            hipLaunchKernelGGL((gemm_f32_persistent_kernel<BM, BN, BK, WAVES_M, WAVES_N, NSTAGE, EPI_BIAS_GELU>), dim3(grid), block, 0, s, a);
             break;
-        case EPI_BIAS_RESID:
-            hipLaunchKernelGGL((gemm_f32_persistent_kernel<BM, BN, BK, WAVES_M, WAVES_N, EPI_BIAS_RESID>), dim3(grid), block, 0, s, a);
+        case EPI_NONE:
+            hipLaunchKernelGGL((gemm_f32_persistent_kernel<BM, BN, BK, WAVES_M, WAVES_N, NSTAGE, EPI_NONE>), dim3(grid), block, 0, s, a);
             break;
         default:
             return hipErrorInvalidValue;
@@ -814,23 +833,26 @@ static hipError_t launch_persistent(const GemmArgs& a, int epi, hipStream_t s, i
 static bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
 
 // fp32 dispatch.  The persistent kernels need 16-byte aligned rows and
-// operands, N % 4 == 0 (float4 epilogue) and K a multiple of their k-tile;
-// anything else takes the guarded register-staged kernel.  Tile choice (c3
-// shapes, MI355X): a 64-deep k-tile with 8 waves for the K = 384 projections,
-// 4 waves for long K (FFN down), and 32-deep with two workgroups per CU for
-// wide outputs (FFN up), where one workgroup's epilogue overlaps the other's MFMAs.
+// operands, N % 4 == 0 (float4 epilogue), K a multiple of their k-tile with
+// at least NSTAGE - 1 k-tiles, and no residual operand; anything else takes
+// the guarded register-staged kernel.
 hipError_t launch_gemm_f32(const GemmArgs& a, int epi, hipStream_t s) {
-    const bool aligned = aligned16(a.A) && aligned16(a.W) && aligned16(a.C) && aligned16(a.bias) &&
-                         (epi != EPI_BIAS_RESID || (aligned16(a.R) && a.ldr % 4 == 0)) &&
-                         a.lda % 4 == 0 && a.ldw % 4 == 0 && a.ldc % 4 == 0 && a.N % 4 == 0;
-    if (aligned && a.K % 64 == 0 && a.K >= 1024)
-        return launch_persistent<128, 128, 64, 2, 2>(a, epi, s, 1);
-    if (aligned && a.K % 32 == 0 && a.N >= 1536)
-        return launch_persistent<128, 128, 32, 2, 4>(a, epi, s, 2);
-    if (aligned && a.K % 64 == 0)
-        return launch_persistent<128, 128, 64, 2, 4>(a, epi, s, 1);
-    if (aligned && a.K % 32 == 0)
-        return launch_persistent<128, 128, 32, 2, 4>(a, epi, s, 2);
+    const bool ok = epi != EPI_BIAS_RESID && aligned16(a.A) && aligned16(a.W) && aligned16(a.C) &&
+                    (epi == EPI_NONE || aligned16(a.bias)) && a.lda % 4 == 0 && a.ldw % 4 == 0 &&
+                    a.ldc % 4 == 0 && a.N % 4 == 0;
+    // Tile choice measured on MI355X at the c3 shapes (M = 32768): 64-deep
+    // k-tiles with two LDS stages and one workgroup per CU; 8 waves for narrow
+    // outputs, 4 for wide; for wide outputs over a short K (FFN up, many tiles
+    // per CU) 32-deep k-tiles and two workgroups per CU, so one workgroup's
+    // epilogue runs beside the other's MFMAs.
+    if (ok && a.K % 32 == 0 && a.N >= 1536 && a.K < 1024)
+        return launch_persistent<128, 128, 32, 2, 2, 2>(a, epi, s, 2);
+    if (ok && a.K % 64 == 0 && a.N <= 512)
+        return launch_persistent<128, 128, 64, 2, 4, 2>(a, epi, s, 1);
+    if (ok && a.K % 64 == 0)
+        return launch_persistent<128, 128, 64, 2, 2, 2>(a, epi, s, 1);
+    if (ok && a.K % 32 == 0)
+        return launch_persistent<128, 128, 32, 2, 2, 2>(a, epi, s, 2);
     return launch_tile<128, 128, 32, 2, 2, false>(a, epi, s);
 }
 

@@ -5,9 +5,10 @@
 
 namespace ebh {
 
-// GEMM epilogues: bias is always added; then optionally GELU (FFN up) or a
-// residual add (attention output and FFN down projections).
-enum Epilogue : int { EPI_BIAS = 0, EPI_BIAS_GELU = 1, EPI_BIAS_RESID = 2 };
+// GEMM epilogues: bias, then optionally GELU (FFN up) or a residual add; or
+// none at all (the forward adds bias and residual of the attention-output and
+// FFN-down projections in the LayerNorm that follows them).
+enum Epilogue : int { EPI_BIAS = 0, EPI_BIAS_GELU = 1, EPI_BIAS_RESID = 2, EPI_NONE = 3 };
 
 struct GemmArgs {
     const void* A;       // [M, K] row-major activations (fp32)
@@ -34,6 +35,11 @@ hipError_t launch_attention(const float* qkv, const int* cu_seqlens, int B, int 
 // Row LayerNorm (population variance), y may alias x.
 hipError_t launch_layernorm(const float* x, float* y, const float* g, const float* b,
                             int rows_max, const int* rows_dev, int H, float eps, hipStream_t s);
+
+// x = LayerNorm((y + bias) + x) per row, in place on x.
+hipError_t launch_add_layernorm(const float* y, const float* bias, float* x, const float* g,
+                                const float* b, int rows_max, const int* rows_dev, int H, float eps,
+                                hipStream_t s);
 
 // Token packing: mask [B,S] -> cu_seqlens [B+1], n_tokens, packed ids/positions.
 hipError_t launch_pack(const int* ids, const int* mask, int B, int S, int* counts, int* cu,

@@ -150,6 +150,31 @@ __global__ __launch_bounds__(256) void layernorm_kernel(const float* x, float* y
     ln_row<NC>(v, lane, H, g, bta, eps, y + (int64_t)row * H);
 }
 
+// Residual block end (BertLayer::forward, src/lib.rs:672-674 and 677-679):
+// x = LayerNorm((y + bias) + x), where y is the projection without its bias
+// (the GEMM writes it raw), added in the reference's order: the Linear's bias
+// first (src/lib.rs:733, 747), then the block input.  In place on x.
+template <int NC>
+__global__ __launch_bounds__(256) void add_layernorm_kernel(const float* __restrict__ y,
+                                                            const float* __restrict__ bias,
+                                                            float* x, const float* __restrict__ g,
+                                                            const float* __restrict__ bta,
+                                                            int rows_max, const int* rows_dev,
+                                                            int H, float eps) {
+    const int row = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+    const int rows = rows_dev ? *rows_dev : rows_max;
+    if (row >= rows) return;
+    const float* yr = y + (int64_t)row * H;
+    float* xr = x + (int64_t)row * H;
+    float v[NC];
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+        const int i = c * 64 + lane;
+        v[c] = i < H ? (yr[i] + bias[i]) + xr[i] : 0.0f;
+    }
+    ln_row<NC>(v, lane, H, g, bta, eps, xr);
+}
+
 // Embeddings (Model::forward, src/lib.rs:628-661): word[id] + position[pos] +
 // token_type[0], then the embeddings LayerNorm.  An id outside [0, V) reads
 // row 0 and raises the error flag (the reference panics on such an id).
@@ -198,6 +223,15 @@ hipError_t launch_layernorm(const float* x, float* y, const float* g, const floa
     return hipGetLastError();
 }
 
+hipError_t launch_add_layernorm(const float* y, const float* bias, float* x, const float* g,
+                                const float* b, int rows_max, const int* rows_dev, int H, float eps,
+                                hipStream_t s) {
+    if (rows_max <= 0) return hipSuccess;
+    const dim3 grid((rows_max + 3) / 4);
+    EBH_ROW_DISPATCH(add_layernorm_kernel, H, grid, s, y, bias, x, g, b, rows_max, rows_dev, H, eps);
+    return hipGetLastError();
+}
+
 hipError_t launch_embed_ln(const int* tok_id, const int* tok_pos, const int* n_tokens,
                            int T_max, const float* word, const float* pos, const float* type0,
                            const float* g, const float* b, int V, int H, float eps, float* x,
@@ -211,22 +245,47 @@ hipError_t launch_embed_ln(const int* tok_id, const int* tok_pos, const int* n_t
 
 // ---------------------------------------------------------------------------
 // mean_pool (src/lib.rs:993-1010) + normalise (src/lib.rs:605-612): one
-// workgroup per sequence; the 4 waves sum interleaved tokens, then wave 0
-// combines, divides by max(count, 1) and optionally scales by
-// 1 / max(||x||, 1e-12).  A sequence with no real token among S > 0
-// positions is NaN, as the reference's all -inf softmax row makes it.
+// 512-thread workgroup per sequence.  Wave w sums tokens w, w+8, w+16, ...
+// with four rows in flight per step (the sum is latency-bound otherwise);
+// wave 0 then adds the eight partial rows in wave order, divides by
+// max(count, 1) and optionally scales by 1 / max(||x||, 1e-12).  The order
+// of additions depends only on the sequence's own length, so a sequence gives
+// the same vector wherever it sits in the batch.  A sequence with no real
+// token among S > 0 positions is NaN, as the reference's all -inf softmax row
+// makes it.
 // ---------------------------------------------------------------------------
+constexpr int POOL_WAVES = 8;
+
 template <int NC>
-__global__ __launch_bounds__(256) void pool_kernel(const float* __restrict__ x,
-                                                   const int* __restrict__ cu, int H, int S,
-                                                   int normalize, float* __restrict__ out) {
-    __shared__ float red[3][NC * 64];
+__global__ __launch_bounds__(64 * POOL_WAVES) void pool_kernel(const float* __restrict__ x,
+                                                               const int* __restrict__ cu, int H,
+                                                               int S, int normalize,
+                                                               float* __restrict__ out) {
+    __shared__ float red[POOL_WAVES - 1][NC * 64];
     const int b = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int start = cu[b], len = cu[b + 1] - start;
     float acc[NC];
 #pragma unroll
     for (int c = 0; c < NC; ++c) acc[c] = 0.0f;
-    for (int t = wave; t < len; t += 4) {
+    constexpr int U = 4;  // rows in flight per wave
+    int t = wave;
+    for (; t + (U - 1) * POOL_WAVES < len; t += U * POOL_WAVES) {
+        float v[U][NC];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const float* xr = x + (int64_t)(start + t + u * POOL_WAVES) * H;
+#pragma unroll
+            for (int c = 0; c < NC; ++c) {
+                const int i = c * 64 + lane;
+                v[u][c] = i < H ? xr[i] : 0.0f;
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u)
+#pragma unroll
+            for (int c = 0; c < NC; ++c) acc[c] += v[u][c];
+    }
+    for (; t < len; t += POOL_WAVES) {
         const float* xr = x + (int64_t)(start + t) * H;
 #pragma unroll
         for (int c = 0; c < NC; ++c) {
@@ -246,7 +305,9 @@ __global__ __launch_bounds__(256) void pool_kernel(const float* __restrict__ x,
 #pragma unroll
     for (int c = 0; c < NC; ++c) {
         const int i = c * 64 + lane;
-        float v = ((acc[c] + red[0][c * 64 + lane]) + red[1][c * 64 + lane]) + red[2][c * 64 + lane];
+        float v = acc[c];
+#pragma unroll
+        for (int w = 0; w < POOL_WAVES - 1; ++w) v += red[w][c * 64 + lane];
         v = v / count;
         if (all_masked) v = __builtin_nanf("");
         acc[c] = v;
@@ -263,7 +324,15 @@ __global__ __launch_bounds__(256) void pool_kernel(const float* __restrict__ x,
 hipError_t launch_pool(const float* x, const int* cu_seqlens, int B, int H, int S, int normalize,
                        float* out, hipStream_t s) {
     if (B <= 0) return hipSuccess;
-    EBH_ROW_DISPATCH(pool_kernel, H, dim3(B), s, x, cu_seqlens, H, S, normalize, out);
+    const int nc = (H + 63) / 64;
+    const dim3 grid(B), block(64 * POOL_WAVES);
+    if (nc <= 4) hipLaunchKernelGGL(pool_kernel<4>, grid, block, 0, s, x, cu_seqlens, H, S, normalize, out);
+    else if (nc <= 6) hipLaunchKernelGGL(pool_kernel<6>, grid, block, 0, s, x, cu_seqlens, H, S, normalize, out);
+    else if (nc <= 8) hipLaunchKernelGGL(pool_kernel<8>, grid, block, 0, s, x, cu_seqlens, H, S, normalize, out);
+    else if (nc <= 12) hipLaunchKernelGGL(pool_kernel<12>, grid, block, 0, s, x, cu_seqlens, H, S, normalize, out);
+    else if (nc <= 16) hipLaunchKernelGGL(pool_kernel<16>, grid, block, 0, s, x, cu_seqlens, H, S, normalize, out);
+    else if (nc <= 32) hipLaunchKernelGGL(pool_kernel<32>, grid, block, 0, s, x, cu_seqlens, H, S, normalize, out);
+    else return hipErrorInvalidValue;
     return hipGetLastError();
 }
 

@@ -24,13 +24,14 @@ extern "C" {
 #define EBH_EPI_BIAS 0       /* C = A.W^T + b                       */
 #define EBH_EPI_BIAS_GELU 1  /* C = gelu_tanh(A.W^T + b)             */
 #define EBH_EPI_BIAS_RESID 2 /* C = (A.W^T + b) + R                  */
+#define EBH_EPI_NONE 3       /* C = A.W^T (bias may be NULL)         */
 
 /* matmul_3d_2d + bias (+ gelu / + residual) (src/lib.rs:795-849, 691-698,
  * 732-733, 741-747, 673, 678, 958-978), batch folded into M:
  * A [M, K] fp32 (row stride lda), W [N, K] HF layout (row stride ldw), fp32
  * when w_dtype == EBH_DTYPE_F32 or bf16 bits (uint16) when EBH_DTYPE_BF16 (A
  * is then rounded to bf16 on load; accumulation is fp32).  C [M, N] (ldc);
- * residual [M, N] (ldr) only for EBH_EPI_BIAS_RESID.  K and the strides must
+ * residual [M, N] (ldr) only for EBH_EPI_BIAS_RESID; bias may be NULL for EBH_EPI_NONE.  K and the strides must
  * be multiples of 4 (fp32) / 8 (bf16). */
 EBH_API int ebh_op_gemm(const float* A, int64_t lda, const void* W, int64_t ldw, int32_t w_dtype,
                 const float* bias, const float* residual, int64_t ldr, float* C, int64_t ldc,
@@ -47,6 +48,12 @@ EBH_API int ebh_op_attention(const float* qkv, const int32_t* cu_seqlens, int32_
 /* apply_layer_norm_3d (src/lib.rs:980-991) over rows x [rows, H] -> y (may alias). */
 EBH_API int ebh_op_layer_norm(const float* x, const float* gamma, const float* beta, int32_t rows,
                       int32_t H, float eps, float* y, void* stream);
+
+/* End of a residual block (src/lib.rs:672-674, 677-679): x = LayerNorm((y + bias)
+ * + x) over rows [rows, H], in place on x; y is a projection written without its
+ * bias (EBH_EPI_NONE).  The additions follow the reference's order. */
+EBH_API int ebh_op_add_layer_norm(const float* y, const float* bias, float* x, const float* gamma,
+                          const float* beta, int32_t rows, int32_t H, float eps, void* stream);
 
 /* mean_pool (src/lib.rs:993-1010) over packed sequences (+ the normalise tail,
  * src/lib.rs:605-612, when normalize != 0); S is the padded length the caller

@@ -55,7 +55,7 @@ GEMM_SHAPES = [(1, 8, 4), (7, 40, 12), (130, 1152, 384), (257, 384, 1536), (64, 
 
 
 @pytest.mark.parametrize("M,N,K", GEMM_SHAPES)
-@pytest.mark.parametrize("epi", [0, 1, 2])
+@pytest.mark.parametrize("epi", [0, 1, 2, 3])
 def test_gemm_f32(env, M, N, K, epi):
     torch, eb, Nn, L = env
     rng = np.random.default_rng(M * 7 + N + K + epi)
@@ -66,10 +66,10 @@ def test_gemm_f32(env, M, N, K, epi):
     R = rng.standard_normal((M, N)).astype(np.float32)
     dA, dW, db, dR = dev(torch, A), dev(torch, W), dev(torch, bias), dev(torch, R)
     dC = torch.full((M, N), float("nan"), device="cuda")
-    Nn.check(L.ebh_op_gemm(vp(dA), lda, vp(dW), K, Nn.EBH_DTYPE_F32, vp(db),
+    Nn.check(L.ebh_op_gemm(vp(dA), lda, vp(dW), K, Nn.EBH_DTYPE_F32, vp(db) if epi != 3 else None,
                            vp(dR) if epi == 2 else None, N, vp(dC), N, M, N, K, epi, stream(torch)))
     torch.cuda.synchronize()
-    want = A[:, :K].astype(np.float64) @ W.T.astype(np.float64) + bias
+    want = A[:, :K].astype(np.float64) @ W.T.astype(np.float64) + (bias if epi != 3 else 0.0)
     if epi == 1:
         want = gelu64(want)
     if epi == 2:
@@ -201,6 +201,26 @@ def test_layer_norm(env, H):
     want = oracle.layer_norm(x, g, b, 1e-12)
     np.testing.assert_allclose(dy.cpu().numpy(), want, rtol=0, atol=1e-5)
     np.testing.assert_array_equal(dx.cpu().numpy(), dy.cpu().numpy())
+
+
+@pytest.mark.parametrize("H", [64, 384, 768])
+def test_add_layer_norm(env, H):
+    """x = LN((y + b) + x), the residual-block end the forward uses."""
+    torch, eb, Nn, L = env
+    import oracle
+    rng = np.random.default_rng(H + 1)
+    rows = 517
+    y = rng.standard_normal((rows, H)).astype(np.float32)
+    x = rng.standard_normal((rows, H)).astype(np.float32)
+    b = rng.standard_normal(H).astype(np.float32)
+    g = rng.standard_normal(H).astype(np.float32)
+    beta = rng.standard_normal(H).astype(np.float32)
+    dy, dx, db, dg, dbeta = (dev(torch, a) for a in (y, x, b, g, beta))
+    Nn.check(L.ebh_op_add_layer_norm(vp(dy), vp(db), vp(dx), vp(dg), vp(dbeta), rows, H,
+                                     ctypes.c_float(1e-12), stream(torch)))
+    torch.cuda.synchronize()
+    want = oracle.layer_norm(((y + b) + x).astype(np.float32), g, beta, 1e-12)
+    np.testing.assert_allclose(dx.cpu().numpy(), want, rtol=0, atol=1e-5)
 
 
 @pytest.mark.parametrize("normalize", [0, 1])
