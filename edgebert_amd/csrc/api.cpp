@@ -69,6 +69,7 @@ struct Workspace {
     int64_t tok_cap = 0;  // B*S tokens
     int b_cap = 0;
     float *X, *Y, *QKV, *CTX, *F;
+    uint16_t* X16;  // bf16 copy of X (bf16 models: the GEMM input)
     int *ids, *mask, *counts, *cu, *ntok, *tok_id, *tok_pos, *err;
     float* out;
 };
@@ -203,7 +204,8 @@ int ensure_workspace(ebh_model* m, int B, int S) {
     const size_t H = c.hidden_size, I = c.intermediate_size;
     size_t off = 0;
     auto take = [&](size_t bytes) { size_t o = off; off += align_up(std::max<size_t>(bytes, 1)); return o; };
-    const size_t oX = take(tcap * H * 4), oY = take(tcap * H * 4), oQKV = take(tcap * 3 * H * 4),
+    const size_t oX = take(tcap * H * 4), oX16 = take(m->dtype == EBH_DTYPE_BF16 ? tcap * H * 2 : 0),
+                 oY = take(tcap * H * 4), oQKV = take(tcap * 3 * H * 4),
                  oCTX = take(tcap * H * 4), oF = take(tcap * I * 4), oIds = take(tcap * 4),
                  oMask = take(tcap * 4), oCounts = take(bcap * 4), oCu = take((bcap + 1) * 4),
                  oNtok = take(4), oTid = take(tcap * 4), oTpos = take(tcap * 4), oErr = take(4),
@@ -221,6 +223,7 @@ int ensure_workspace(ebh_model* m, int B, int S) {
     w.tok_cap = tcap;
     w.b_cap = bcap;
     w.X = (float*)(b + oX);
+    w.X16 = m->dtype == EBH_DTYPE_BF16 ? (uint16_t*)(b + oX16) : nullptr;
     w.Y = (float*)(b + oY);
     w.QKV = (float*)(b + oQKV);
     w.CTX = (float*)(b + oCTX);
@@ -273,25 +276,31 @@ int enqueue_forward(ebh_model* m, const int* d_ids, const int* d_mask, int B, in
 
     ProfPair pp{};
     bool on = false;
+    const bool bf16 = m->dtype == EBH_DTYPE_BF16;
     HIP_TRY(ebh::launch_pack(d_ids, d_mask, B, S, w.counts, w.cu, w.ntok, w.tok_id, w.tok_pos,
                              w.err, s));
     prof_begin(m, EBH_PROF_EMBED, s, pp, on);
     HIP_TRY(ebh::launch_embed_ln(w.tok_id, w.tok_pos, w.ntok, T, m->word, m->pos, m->type0,
-                                 m->emb_g, m->emb_b, c.vocab_size, H, eps, w.X, w.err, s));
+                                 m->emb_g, m->emb_b, c.vocab_size, H, eps, w.X, w.err, w.X16, s));
     prof_end(m, s, pp, on);
 
-    const bool bf16 = m->dtype == EBH_DTYPE_BF16;
-    auto gemm = [&](int kind, const float* A, const float* W32, const uint16_t* W16,
-                    const float* bias, const float* R, float* C, int N, int K, int epi) -> int {
+    // bf16 models keep the residual stream X in fp32 (LayerNorm, softmax and
+    // every sum stay fp32) and hand the GEMMs bf16 operands: X16 (written by
+    // each LayerNorm), the attention context and the GELU output, each stored
+    // as bf16 in the first half of its fp32 buffer.
+    uint16_t* ctx16 = reinterpret_cast<uint16_t*>(w.CTX);
+    uint16_t* f16 = reinterpret_cast<uint16_t*>(w.F);
+    auto gemm = [&](int kind, const void* A, int64_t lda, const float* W32, const uint16_t* W16,
+                    const float* bias, void* C, int N, int K, int epi, bool c16) -> int {
         ebh::GemmArgs a{};
         a.A = A;
         a.W = bf16 ? (const void*)W16 : (const void*)W32;
         a.bias = bias;
-        a.R = R;
-        a.C = C;
-        a.lda = K;
+        a.R = nullptr;
+        a.C = static_cast<float*>(C);
+        a.lda = lda;
         a.ldw = K;
-        a.ldr = N;
+        a.ldr = 0;
         a.ldc = N;
         a.M_max = T;
         a.M_dev = w.ntok;
@@ -300,7 +309,7 @@ int enqueue_forward(ebh_model* m, const int* d_ids, const int* d_mask, int B, in
         ProfPair p2{};
         bool on2 = false;
         prof_begin(m, kind, s, p2, on2);
-        hipError_t e = bf16 ? ebh::launch_gemm_bf16(a, epi, s) : ebh::launch_gemm_f32(a, epi, s);
+        hipError_t e = bf16 ? ebh::launch_gemm_bf16_act(a, epi, c16, s) : ebh::launch_gemm_f32(a, epi, s);
         prof_end(m, s, p2, on2);
         if (e != hipSuccess) return fail(EBH_ERR_HIP, "gemm launch failed: %s", hipGetErrorString(e));
         return EBH_OK;
@@ -311,26 +320,27 @@ int enqueue_forward(ebh_model* m, const int* d_ids, const int* d_mask, int B, in
     // residual are added, in the reference's order, by the LayerNorm that follows.
     for (const DevLayer& L : m->layers) {
         int rc;
-        if ((rc = gemm(EBH_PROF_GEMM_QKV, w.X, L.wqkv, L.wqkv16, L.bqkv, nullptr, w.QKV, 3 * H, H,
-                       ebh::EPI_BIAS)))
+        if ((rc = gemm(EBH_PROF_GEMM_QKV, bf16 ? (const void*)w.X16 : w.X, H, L.wqkv, L.wqkv16, L.bqkv,
+                       w.QKV, 3 * H, H, ebh::EPI_BIAS, false)))
             return rc;
         prof_begin(m, EBH_PROF_ATTENTION, s, pp, on);
-        HIP_TRY(ebh::launch_attention(w.QKV, w.cu, B, S, H, nh, hd, scale, w.CTX, s));
+        HIP_TRY(ebh::launch_attention(w.QKV, w.cu, B, S, H, nh, hd, scale,
+                                      bf16 ? (void*)ctx16 : (void*)w.CTX, bf16, s));
         prof_end(m, s, pp, on);
-        if ((rc = gemm(EBH_PROF_GEMM_OUT, w.CTX, L.wo, L.wo16, nullptr, nullptr, w.Y, H, H,
-                       ebh::EPI_NONE)))
+        if ((rc = gemm(EBH_PROF_GEMM_OUT, bf16 ? (const void*)ctx16 : w.CTX, H, L.wo, L.wo16, nullptr,
+                       w.Y, H, H, ebh::EPI_NONE, false)))
             return rc;
         prof_begin(m, EBH_PROF_LAYERNORM, s, pp, on);
-        HIP_TRY(ebh::launch_add_layernorm(w.Y, L.bo, w.X, L.ln1_g, L.ln1_b, T, w.ntok, H, eps, s));
+        HIP_TRY(ebh::launch_add_layernorm(w.Y, L.bo, w.X, L.ln1_g, L.ln1_b, T, w.ntok, H, eps, w.X16, s));
         prof_end(m, s, pp, on);
-        if ((rc = gemm(EBH_PROF_GEMM_FFN_UP, w.X, L.w1, L.w116, L.b1, nullptr, w.F, I, H,
-                       ebh::EPI_BIAS_GELU)))
+        if ((rc = gemm(EBH_PROF_GEMM_FFN_UP, bf16 ? (const void*)w.X16 : w.X, H, L.w1, L.w116, L.b1,
+                       bf16 ? (void*)f16 : (void*)w.F, I, H, ebh::EPI_BIAS_GELU, bf16)))
             return rc;
-        if ((rc = gemm(EBH_PROF_GEMM_FFN_DOWN, w.F, L.w2, L.w216, nullptr, nullptr, w.Y, H, I,
-                       ebh::EPI_NONE)))
+        if ((rc = gemm(EBH_PROF_GEMM_FFN_DOWN, bf16 ? (const void*)f16 : w.F, I, L.w2, L.w216, nullptr,
+                       w.Y, H, I, ebh::EPI_NONE, false)))
             return rc;
         prof_begin(m, EBH_PROF_LAYERNORM, s, pp, on);
-        HIP_TRY(ebh::launch_add_layernorm(w.Y, L.b2, w.X, L.ln2_g, L.ln2_b, T, w.ntok, H, eps, s));
+        HIP_TRY(ebh::launch_add_layernorm(w.Y, L.b2, w.X, L.ln2_g, L.ln2_b, T, w.ntok, H, eps, w.X16, s));
         prof_end(m, s, pp, on);
     }
     prof_begin(m, EBH_PROF_POOL, s, pp, on);
@@ -424,6 +434,8 @@ int ebh_finalize(ebh_model* m, int32_t dtype) {
     if (m->finalized) return fail(EBH_ERR_STATE, "model already finalized");
     if (dtype != EBH_DTYPE_F32 && dtype != EBH_DTYPE_BF16)
         return fail(EBH_ERR_INVALID_ARG, "unknown dtype %d", dtype);
+    if (dtype == EBH_DTYPE_BF16 && (m->cfg.hidden_size % 64 || m->cfg.intermediate_size % 64))
+        return fail(EBH_ERR_INVALID_ARG, "bf16 models need hidden_size and intermediate_size multiples of 64");
     const auto names = expected_tensors(m->cfg);
     for (auto& kv : names)
         if (!m->host.count(kv.first)) return fail(EBH_ERR_NOT_FOUND, "Tensor %s not found", kv.first.c_str());
@@ -733,6 +745,30 @@ int ebh_op_gemm(const float* A, int64_t lda, const void* W, int64_t ldw, int32_t
     return EBH_OK;
 }
 
+int ebh_op_gemm_bf16(const uint16_t* A, int64_t lda, const uint16_t* W, int64_t ldw,
+                     const float* bias, void* C, int64_t ldc, int32_t c_dtype, int32_t M, int32_t N,
+                     int32_t K, int32_t epilogue, void* stream) {
+    if (!A || !W || !C || (!bias && epilogue != EBH_EPI_NONE)) return fail(EBH_ERR_INVALID_ARG, "null buffer");
+    if (M < 0 || N <= 0 || K <= 0) return fail(EBH_ERR_INVALID_ARG, "bad GEMM shape");
+    if (epilogue != EBH_EPI_BIAS && epilogue != EBH_EPI_BIAS_GELU && epilogue != EBH_EPI_NONE)
+        return fail(EBH_ERR_INVALID_ARG, "epilogue %d not supported with bf16 activations", epilogue);
+    if (c_dtype != EBH_DTYPE_F32 && c_dtype != EBH_DTYPE_BF16)
+        return fail(EBH_ERR_INVALID_ARG, "unknown output dtype %d", c_dtype);
+    if (K % 64 || N % 4 || lda % 8 || ldw % 8 || ldc % 4 || lda < K || ldw < K || ldc < N)
+        return fail(EBH_ERR_INVALID_ARG, "K must be a multiple of 64, N of 4, strides of 8 / 8 / 4");
+    if (((uintptr_t)A | (uintptr_t)W | (uintptr_t)C | (uintptr_t)bias) & 15)
+        return fail(EBH_ERR_INVALID_ARG, "operands must be 16-byte aligned");
+    if (M == 0) return EBH_OK;
+    ebh::GemmArgs a{};
+    a.A = A; a.W = W; a.bias = bias; a.R = nullptr; a.C = static_cast<float*>(C);
+    a.lda = lda; a.ldw = ldw; a.ldr = 0; a.ldc = ldc;
+    a.M_max = M; a.M_dev = nullptr; a.N = N; a.K = K;
+    hipError_t e = ebh::launch_gemm_bf16_act(a, epilogue, c_dtype == EBH_DTYPE_BF16,
+                                             static_cast<hipStream_t>(stream));
+    if (e != hipSuccess) return fail(EBH_ERR_HIP, "gemm launch failed: %s", hipGetErrorString(e));
+    return EBH_OK;
+}
+
 int ebh_op_attention(const float* qkv, const int32_t* cu_seqlens, int32_t B, int32_t max_len,
                      int32_t hidden, int32_t num_heads, float* ctx, void* stream) {
     if (!qkv || !cu_seqlens || !ctx) return fail(EBH_ERR_INVALID_ARG, "null buffer");
@@ -742,7 +778,7 @@ int ebh_op_attention(const float* qkv, const int32_t* cu_seqlens, int32_t B, int
     if (hd != 32 && hd != 64) return fail(EBH_ERR_INVALID_ARG, "head_dim %d unsupported", hd);
     const float scale = 1.0f / sqrtf((float)hd);
     HIP_TRY(ebh::launch_attention(qkv, cu_seqlens, B, max_len, hidden, num_heads, hd, scale, ctx,
-                                  static_cast<hipStream_t>(stream)));
+                                  false, static_cast<hipStream_t>(stream)));
     return EBH_OK;
 }
 
@@ -759,7 +795,7 @@ int ebh_op_add_layer_norm(const float* y, const float* bias, float* x, const flo
                           const float* beta, int32_t rows, int32_t H, float eps, void* stream) {
     if (!y || !bias || !x || !gamma || !beta) return fail(EBH_ERR_INVALID_ARG, "null buffer");
     if (rows < 0 || H <= 0 || H > 2048) return fail(EBH_ERR_INVALID_ARG, "bad LayerNorm shape");
-    HIP_TRY(ebh::launch_add_layernorm(y, bias, x, gamma, beta, rows, nullptr, H, eps,
+    HIP_TRY(ebh::launch_add_layernorm(y, bias, x, gamma, beta, rows, nullptr, H, eps, nullptr,
                                       static_cast<hipStream_t>(stream)));
     return EBH_OK;
 }
@@ -792,7 +828,7 @@ int ebh_op_embed_ln(const int32_t* tok_id, const int32_t* tok_pos, const int32_t
         return fail(EBH_ERR_INVALID_ARG, "null buffer");
     if (T_max < 0 || V <= 0 || H <= 0 || H > 2048) return fail(EBH_ERR_INVALID_ARG, "bad embed shape");
     HIP_TRY(ebh::launch_embed_ln(tok_id, tok_pos, n_tokens, T_max, word, pos, type0, gamma, beta,
-                                 V, H, eps, x, err, static_cast<hipStream_t>(stream)));
+                                 V, H, eps, x, err, nullptr, static_cast<hipStream_t>(stream)));
     return EBH_OK;
 }
 

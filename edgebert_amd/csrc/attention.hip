@@ -27,10 +27,10 @@ namespace ebh {
 typedef float v16f __attribute__((ext_vector_type(16)));
 typedef float v4f __attribute__((ext_vector_type(4)));
 
-template <int HD>
+template <int HD, bool OUT16>
 __global__ __launch_bounds__(256) void attention_kernel(const float* __restrict__ qkv,
                                                         const int* __restrict__ cu_seqlens,
-                                                        float* __restrict__ ctx, int H,
+                                                        void* __restrict__ ctx_out, int H,
                                                         float scale) {
     constexpr int KC = 128;        // keys per LDS chunk
     constexpr int KS = HD + 4;     // K row stride (floats): conflict-free 16-B reads
@@ -159,21 +159,30 @@ __global__ __launch_bounds__(256) void attention_kernel(const float* __restrict_
         const float lq = __shfl(l_tot, qrow);
         const int q = q0 + qrow;
         if (q < len) {
-            float* dst = ctx + (int64_t)(start + q) * H + head * HD + l32;
+            const int64_t at = (int64_t)(start + q) * H + head * HD + l32;
 #pragma unroll
-            for (int j = 0; j < NJ; ++j) dst[j * 32] = o[j][r] / lq;
+            for (int j = 0; j < NJ; ++j) {
+                const float c = o[j][r] / lq;
+                if constexpr (OUT16) static_cast<uint16_t*>(ctx_out)[at + j * 32] = f32_to_bf16_rne(c);
+                else static_cast<float*>(ctx_out)[at + j * 32] = c;
+            }
         }
     }
 }
 
 hipError_t launch_attention(const float* qkv, const int* cu_seqlens, int B, int max_len, int H,
-                            int nh, int head_dim, float scale, float* ctx, hipStream_t s) {
+                            int nh, int head_dim, float scale, void* ctx, bool ctx_bf16,
+                            hipStream_t s) {
     if (B <= 0 || max_len <= 0) return hipSuccess;
     const dim3 grid(nh, (max_len + 127) / 128, B), block(256);
-    if (head_dim == 32)
-        hipLaunchKernelGGL(attention_kernel<32>, grid, block, 0, s, qkv, cu_seqlens, ctx, H, scale);
+    if (head_dim == 32 && !ctx_bf16)
+        hipLaunchKernelGGL((attention_kernel<32, false>), grid, block, 0, s, qkv, cu_seqlens, ctx, H, scale);
+    else if (head_dim == 32)
+        hipLaunchKernelGGL((attention_kernel<32, true>), grid, block, 0, s, qkv, cu_seqlens, ctx, H, scale);
+    else if (head_dim == 64 && !ctx_bf16)
+        hipLaunchKernelGGL((attention_kernel<64, false>), grid, block, 0, s, qkv, cu_seqlens, ctx, H, scale);
     else if (head_dim == 64)
-        hipLaunchKernelGGL(attention_kernel<64>, grid, block, 0, s, qkv, cu_seqlens, ctx, H, scale);
+        hipLaunchKernelGGL((attention_kernel<64, true>), grid, block, 0, s, qkv, cu_seqlens, ctx, H, scale);
     else
         return hipErrorInvalidValue;
     return hipGetLastError();

@@ -375,7 +375,7 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_f32_dtl_kernel(Ge
 // row-contiguous float4.  Its stores are then older than every load still to
 // be waited for, so no later wait depends on them finishing early.
 // ---------------------------------------------------------------------------
-__device__ __forceinline__ void load_lds16_async(const float* g, const float* lds) {
+__device__ __forceinline__ void load_lds16_async(const void* g, const float* lds) {
     const uint32_t base = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)lds);
     uint32_t saved;
     asm volatile(
@@ -428,21 +428,29 @@ __device__ __forceinline__ float gelu_tanh_fast(float val) {
     return val * 0.5f * (1.0f + t);
 }
 
-template <int BM, int BN, int BK, int WAVES_M, int WAVES_N, int NSTAGE, int EPI>
-__global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_f32_persistent_kernel(GemmArgs p) {
+// BF16: A and W are bf16 (16-byte chunk = 8 elements, one
+// v_mfma_f32_32x32x16_bf16 per fragment pair and k-slice); otherwise fp32
+// (chunk = 4 elements, four v_mfma_f32_32x32x2_f32).  OUT16: C is written as
+// bf16 (round to nearest even) instead of fp32.  LDS offsets below are in
+// 4-byte words, so both element types share the layout and the swizzle.
+template <bool BF16, bool OUT16, int BM, int BN, int BK, int WAVES_M, int WAVES_N, int NSTAGE, int EPI>
+__global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_persistent_kernel(GemmArgs p) {
+    constexpr int ES = BF16 ? 2 : 4;              // bytes per element
+    constexpr int EPC = 16 / ES;                  // elements per 16-byte chunk
     static_assert(EPI == EPI_BIAS || EPI == EPI_BIAS_GELU || EPI == EPI_NONE, "no residual here");
     constexpr bool HAS_BIAS = EPI != EPI_NONE;
     constexpr int NT = 64 * WAVES_M * WAVES_N, NW = WAVES_M * WAVES_N;
     constexpr int WM = BM / WAVES_M, WN = BN / WAVES_N;
     constexpr int FM = WM / 32, FN = WN / 32;
     static_assert(FM * 32 == WM && FN * 32 == WN, "wave tile must be whole 32x32 blocks");
-    constexpr int CPR = BK / 4;                   // 16-byte chunks per tile row
-    constexpr int KS = BK / 8;                    // 8-wide k slices per k-tile
+    constexpr int CPR = BK / EPC;                 // 16-byte chunks per tile row
+    constexpr int KS = CPR / 2;                   // k-slices (two chunks: one per lane half)
+    constexpr int RW = CPR * 4;                   // words per tile row
     constexpr int A_CH = BM * CPR, W_CH = BN * CPR;
     static_assert(A_CH % NT == 0 && W_CH % NT == 0, "every wave issues the same loads");
     constexpr int LA = A_CH / NT, LW = W_CH / NT, NL = LA + LW;
     constexpr int D = NSTAGE - 1;                 // k-tiles in flight ahead
-    constexpr int STAGE = (BM + BN) * BK;         // floats per stage: A rows, then W rows
+    constexpr int STAGE = (BM + BN) * RW;         // words per stage: A rows, then W rows
     static_assert(NW * 32 * WN <= STAGE, "each wave transposes 32 C rows at a time through one stage");
     constexpr int C4 = WN / 4;                    // float4 per wave-tile row
     constexpr int RPP = 64 / C4;                  // wave-tile rows per float4 pass
@@ -468,8 +476,8 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_f32_persistent_ke
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int wm = wave / WAVES_N, wn = wave % WAVES_N;
     const int l32 = lane & 31, half = lane >> 5;
-    const float* __restrict__ A = static_cast<const float*>(p.A);
-    const float* __restrict__ W = static_cast<const float*>(p.W);
+    const char* __restrict__ A = static_cast<const char*>(p.A);
+    const char* __restrict__ W = static_cast<const char*>(p.W);
 
     // This lane's share of each k-tile load: row and swizzled k-chunk of LDS chunk i*NT + tid.
     int l_r[NL], l_c[NL];
@@ -477,11 +485,11 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_f32_persistent_ke
     for (int i = 0; i < NL; ++i) {
         const int P = (i < LA ? i : i - LA) * NT + tid;
         l_r[i] = P / CPR;
-        l_c[i] = 4 * ((P % CPR) ^ chunk_swizzle16<CPR>(P / CPR));
+        l_c[i] = EPC * ((P % CPR) ^ chunk_swizzle16<CPR>(P / CPR));   // elements
     }
     // Source pointers of the next k-tile to load (iteration `nit`), advanced by BK
     // per k-tile and recomputed when that k-tile starts a new C tile.
-    const float* src[NL];
+    const char* src[NL];                          // byte addresses
     const float* bias_src = nullptr;
     int nit = 0;
     auto point_at = [&](int it) {
@@ -489,8 +497,8 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_f32_persistent_ke
         const int mt = t / ntiles_n, m0 = mt * BM, n0 = (t - mt * ntiles_n) * BN;
 #pragma unroll
         for (int i = 0; i < NL; ++i)
-            src[i] = i < LA ? A + (int64_t)min(m0 + l_r[i], M - 1) * p.lda + kt * BK + l_c[i]
-                            : W + (int64_t)min(n0 + l_r[i], N - 1) * p.ldw + kt * BK + l_c[i];
+            src[i] = i < LA ? A + ((int64_t)min(m0 + l_r[i], M - 1) * p.lda + kt * BK + l_c[i]) * ES
+                            : W + ((int64_t)min(n0 + l_r[i], N - 1) * p.ldw + kt * BK + l_c[i]) * ES;
         if (HAS_BIAS) bias_src = p.bias + min(n0 + wn * WN + 4 * lane, N - 4);
     };
     // Load instructions of k-tile j (the bias chunk rides with a tile's first k-tile).
@@ -499,7 +507,7 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_f32_persistent_ke
         float* st = smem + (nit % NSTAGE) * STAGE;
 #pragma unroll
         for (int i = 0; i < NL; ++i)
-            load_lds16_async(src[i], st + (i < LA ? 0 : BM * BK) + ((i < LA ? i : i - LA) * NT + wave * 64) * 4);
+            load_lds16_async(src[i], st + (i < LA ? 0 : BM * RW) + ((i < LA ? i : i - LA) * NT + wave * 64) * 4);
         if (HAS_BIAS && nit % nk == 0)
             load_lds16_async(bias_src, smem + NSTAGE * STAGE + (((nit / nk) & 1) * NW + wave) * BIAS_SLOT);
         ++nit;
@@ -508,13 +516,13 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_f32_persistent_ke
                 point_at(nit);
             } else {
 #pragma unroll
-                for (int i = 0; i < NL; ++i) src[i] += BK;
+                for (int i = 0; i < NL; ++i) src[i] += BK * ES;
             }
         }
     };
 
     const int sw = chunk_swizzle16<CPR>(l32);
-    const int a_row = (wm * WM + l32) * BK, w_row = BM * BK + (wn * WN + l32) * BK;
+    const int a_row = (wm * WM + l32) * RW, w_row = BM * RW + (wn * WN + l32) * RW;
     // Epilogue lane map: pass qq of block row i covers wave-tile rows
     // i*32 + qq*RPP + lane / C4, columns 4 * (lane % C4) .. +3.
     const int e_r = lane / C4, e_c = 4 * (lane % C4);
@@ -547,7 +555,16 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_f32_persistent_ke
                     v.z = gelu_tanh_fast(v.z); v.w = gelu_tanh_fast(v.w);
                 }
                 const int row = grow0 + i * 32 + qq * RPP;
-                if (col_ok && row < M) *reinterpret_cast<float4*>(p.C + (int64_t)row * p.ldc + gc) = v;
+                if (col_ok && row < M) {
+                    if constexpr (OUT16) {
+                        uint2 h;
+                        h.x = (uint32_t)f32_to_bf16_rne(v.x) | ((uint32_t)f32_to_bf16_rne(v.y) << 16);
+                        h.y = (uint32_t)f32_to_bf16_rne(v.z) | ((uint32_t)f32_to_bf16_rne(v.w) << 16);
+                        *reinterpret_cast<uint2*>(reinterpret_cast<uint16_t*>(p.C) + (int64_t)row * p.ldc + gc) = h;
+                    } else {
+                        *reinterpret_cast<float4*>(p.C + (int64_t)row * p.ldc + gc) = v;
+                    }
+                }
             }
         }
     };
@@ -584,18 +601,27 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_f32_persistent_ke
                 v4f af[FM], wf[FN];
 #pragma unroll
                 for (int i = 0; i < FM; ++i)
-                    af[i] = *reinterpret_cast<const v4f*>(st + a_row + i * 32 * BK + ko);
+                    af[i] = *reinterpret_cast<const v4f*>(st + a_row + i * 32 * RW + ko);
 #pragma unroll
                 for (int j = 0; j < FN; ++j)
-                    wf[j] = *reinterpret_cast<const v4f*>(st + w_row + j * 32 * BK + ko);
-#pragma unroll
-                for (int q = 0; q < 4; ++q)
+                    wf[j] = *reinterpret_cast<const v4f*>(st + w_row + j * 32 * RW + ko);
+                if constexpr (BF16) {
 #pragma unroll
                     for (int i = 0; i < FM; ++i)
 #pragma unroll
                         for (int j = 0; j < FN; ++j)
-                            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(af[i][q], wf[j][q],
-                                                                             acc[i][j], 0, 0, 0);
+                            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+                                __builtin_bit_cast(v8bf, af[i]), __builtin_bit_cast(v8bf, wf[j]), acc[i][j], 0, 0, 0);
+                } else {
+#pragma unroll
+                    for (int q = 0; q < 4; ++q)
+#pragma unroll
+                        for (int i = 0; i < FM; ++i)
+#pragma unroll
+                            for (int j = 0; j < FN; ++j)
+                                acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(af[i][q], wf[j][q],
+                                                                                 acc[i][j], 0, 0, 0);
+                }
             }
         }
     }
@@ -808,7 +834,7 @@ static int cu_count() {
     return n;
 }
 
-template <int BM, int BN, int BK, int WAVES_M, int WAVES_N, int NSTAGE>
+template <int BM, int BN, int BK, int WAVES_M, int WAVES_N, int NSTAGE, bool BF16 = false, bool OUT16 = false>
 static hipError_t launch_persistent(const GemmArgs& a, int epi, hipStream_t s, int wg_per_cu = 1) {
     const int64_t tiles = (int64_t)((a.M_max + BM - 1) / BM) * ((a.N + BN - 1) / BN);
     if (tiles == 0) return hipSuccess;
@@ -816,13 +842,13 @@ static hipError_t launch_persistent(const GemmArgs& a, int epi, hipStream_t s, i
     const dim3 block(64 * WAVES_M * WAVES_N);
     switch (epi) {
         case EPI_BIAS:
-            hipLaunchKernelGGL((gemm_f32_persistent_kernel<BM, BN, BK, WAVES_M, WAVES_N, NSTAGE, EPI_BIAS>), dim3(grid), block, 0, s, a);
+            hipLaunchKernelGGL((gemm_persistent_kernel<BF16, OUT16, BM, BN, BK, WAVES_M, WAVES_N, NSTAGE, EPI_BIAS>), dim3(grid), block, 0, s, a);
             break;
         case EPI_BIAS_GELU:
-            hipLaunchKernelGGL((gemm_f32_persistent_kernel<BM, BN, BK, WAVES_M, WAVES_N, NSTAGE, EPI_BIAS_GELU>), dim3(grid), block, 0, s, a);
+            hipLaunchKernelGGL((gemm_persistent_kernel<BF16, OUT16, BM, BN, BK, WAVES_M, WAVES_N, NSTAGE, EPI_BIAS_GELU>), dim3(grid), block, 0, s, a);
             break;
         case EPI_NONE:
-            hipLaunchKernelGGL((gemm_f32_persistent_kernel<BM, BN, BK, WAVES_M, WAVES_N, NSTAGE, EPI_NONE>), dim3(grid), block, 0, s, a);
+            hipLaunchKernelGGL((gemm_persistent_kernel<BF16, OUT16, BM, BN, BK, WAVES_M, WAVES_N, NSTAGE, EPI_NONE>), dim3(grid), block, 0, s, a);
             break;
         default:
             return hipErrorInvalidValue;
@@ -854,6 +880,17 @@ hipError_t launch_gemm_f32(const GemmArgs& a, int epi, hipStream_t s) {
     if (ok && a.K % 32 == 0)
         return launch_persistent<128, 128, 32, 2, 2, 2>(a, epi, s, 2);
     return launch_tile<128, 128, 32, 2, 2, false>(a, epi, s);
+}
+
+// bf16 activations: 256 x 256 tiles, 64-deep k-tiles (8 chunks of 8), 8 waves
+// of 128 x 64, two LDS stages (2 x 64 KB), one workgroup per CU.
+hipError_t launch_gemm_bf16_act(const GemmArgs& a, int epi, bool c_bf16, hipStream_t s) {
+    const bool ok = epi != EPI_BIAS_RESID && aligned16(a.A) && aligned16(a.W) && aligned16(a.C) &&
+                    (epi == EPI_NONE || aligned16(a.bias)) && a.lda % 8 == 0 && a.ldw % 8 == 0 &&
+                    a.ldc % 4 == 0 && a.N % 4 == 0 && a.K % 64 == 0 && a.K > 0;
+    if (!ok) return hipErrorInvalidValue;
+    if (c_bf16) return launch_persistent<256, 256, 64, 2, 4, 2, true, true>(a, epi, s, 1);
+    return launch_persistent<256, 256, 64, 2, 4, 2, true, false>(a, epi, s, 1);
 }
 
 hipError_t launch_gemm_bf16(const GemmArgs& a, int epi, hipStream_t s) {

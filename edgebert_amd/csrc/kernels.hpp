@@ -27,19 +27,26 @@ hipError_t launch_gemm_f32(const GemmArgs& a, int epi, hipStream_t s);
 hipError_t launch_gemm_bf16(const GemmArgs& a, int epi, hipStream_t s);
 
 // Masked multi-head attention over packed sequences: qkv [T, 3H] rows
-// (q | k | v), cu_seqlens [B+1]; ctx [T, H].  head_dim 32 or 64.
+// (q | k | v), cu_seqlens [B+1]; ctx [T, H] fp32, or bf16 bits when ctx_bf16.
+// head_dim 32 or 64.
 hipError_t launch_attention(const float* qkv, const int* cu_seqlens, int B, int max_len,
-                            int H, int nh, int head_dim, float scale, float* ctx,
+                            int H, int nh, int head_dim, float scale, void* ctx, bool ctx_bf16,
                             hipStream_t s);
+
+// bf16 activations and weights, fp32 accumulate: C = epi(A . W^T + bias), A [M,K]
+// and W [N,K] bf16 bits, C fp32 or (c_bf16) bf16 bits.  Needs 16-byte aligned
+// operands and rows, N % 4 == 0 and K % 64 == 0 (hipErrorInvalidValue otherwise).
+hipError_t launch_gemm_bf16_act(const GemmArgs& a, int epi, bool c_bf16, hipStream_t s);
 
 // Row LayerNorm (population variance), y may alias x.
 hipError_t launch_layernorm(const float* x, float* y, const float* g, const float* b,
                             int rows_max, const int* rows_dev, int H, float eps, hipStream_t s);
 
 // x = LayerNorm((y + bias) + x) per row, in place on x.
+// x16 (optional): bf16 copy of the result (the input of bf16 GEMMs).
 hipError_t launch_add_layernorm(const float* y, const float* bias, float* x, const float* g,
                                 const float* b, int rows_max, const int* rows_dev, int H, float eps,
-                                hipStream_t s);
+                                uint16_t* x16, hipStream_t s);
 
 // Token packing: mask [B,S] -> cu_seqlens [B+1], n_tokens, packed ids/positions.
 hipError_t launch_pack(const int* ids, const int* mask, int B, int S, int* counts, int* cu,
@@ -49,7 +56,7 @@ hipError_t launch_pack(const int* ids, const int* mask, int B, int S, int* count
 hipError_t launch_embed_ln(const int* tok_id, const int* tok_pos, const int* n_tokens,
                            int T_max, const float* word, const float* pos, const float* type0,
                            const float* g, const float* b, int V, int H, float eps, float* x,
-                           int* err, hipStream_t s);
+                           int* err, uint16_t* x16, hipStream_t s);
 
 // Masked mean over each packed sequence, optional L2 normalisation; out [B, H].
 hipError_t launch_pool(const float* x, const int* cu_seqlens, int B, int H, int S,

@@ -110,7 +110,8 @@ hipError_t launch_pack(const int* ids, const int* mask, int B, int S, int* count
 // ---------------------------------------------------------------------------
 template <int NC>
 __device__ __forceinline__ void ln_row(float (&v)[NC], int lane, int H, const float* g,
-                                       const float* b, float eps, float* y) {
+                                       const float* b, float eps, float* y,
+                                       uint16_t* y16 = nullptr) {
     float s = 0.0f;
 #pragma unroll
     for (int c = 0; c < NC; ++c) s += v[c];
@@ -127,7 +128,11 @@ __device__ __forceinline__ void ln_row(float (&v)[NC], int lane, int H, const fl
 #pragma unroll
     for (int c = 0; c < NC; ++c) {
         const int i = c * 64 + lane;
-        if (i < H) y[i] = (v[c] - mean) * inv_std * g[i] + b[i];
+        if (i < H) {
+            const float o = (v[c] - mean) * inv_std * g[i] + b[i];
+            y[i] = o;
+            if (y16) y16[i] = f32_to_bf16_rne(o);  // bf16 copy for bf16 GEMM inputs
+        }
     }
 }
 
@@ -160,7 +165,7 @@ __global__ __launch_bounds__(256) void add_layernorm_kernel(const float* __restr
                                                             float* x, const float* __restrict__ g,
                                                             const float* __restrict__ bta,
                                                             int rows_max, const int* rows_dev,
-                                                            int H, float eps) {
+                                                            int H, float eps, uint16_t* x16) {
     const int row = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
     const int rows = rows_dev ? *rows_dev : rows_max;
     if (row >= rows) return;
@@ -172,7 +177,7 @@ __global__ __launch_bounds__(256) void add_layernorm_kernel(const float* __restr
         const int i = c * 64 + lane;
         v[c] = i < H ? (yr[i] + bias[i]) + xr[i] : 0.0f;
     }
-    ln_row<NC>(v, lane, H, g, bta, eps, xr);
+    ln_row<NC>(v, lane, H, g, bta, eps, xr, x16 ? x16 + (int64_t)row * H : nullptr);
 }
 
 // Embeddings (Model::forward, src/lib.rs:628-661): word[id] + position[pos] +
@@ -184,7 +189,7 @@ __global__ __launch_bounds__(256) void embed_ln_kernel(
     const int* __restrict__ n_tokens, const float* __restrict__ word,
     const float* __restrict__ pos, const float* __restrict__ type0, const float* __restrict__ g,
     const float* __restrict__ bta, int V, int H, float eps, float* __restrict__ x,
-    int* __restrict__ err) {
+    int* __restrict__ err, uint16_t* __restrict__ x16) {
     const int t = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
     if (t >= *n_tokens) return;
     int id = tok_id[t];
@@ -200,7 +205,7 @@ __global__ __launch_bounds__(256) void embed_ln_kernel(
         const int i = c * 64 + lane;
         v[c] = i < H ? (wr[i] + pr[i]) + type0[i] : 0.0f;
     }
-    ln_row<NC>(v, lane, H, g, bta, eps, x + (int64_t)t * H);
+    ln_row<NC>(v, lane, H, g, bta, eps, x + (int64_t)t * H, x16 ? x16 + (int64_t)t * H : nullptr);
 }
 
 #define EBH_ROW_DISPATCH(KERNEL, H, GRID, STREAM, ...)                                       \
@@ -225,21 +230,21 @@ hipError_t launch_layernorm(const float* x, float* y, const float* g, const floa
 
 hipError_t launch_add_layernorm(const float* y, const float* bias, float* x, const float* g,
                                 const float* b, int rows_max, const int* rows_dev, int H, float eps,
-                                hipStream_t s) {
+                                uint16_t* x16, hipStream_t s) {
     if (rows_max <= 0) return hipSuccess;
     const dim3 grid((rows_max + 3) / 4);
-    EBH_ROW_DISPATCH(add_layernorm_kernel, H, grid, s, y, bias, x, g, b, rows_max, rows_dev, H, eps);
+    EBH_ROW_DISPATCH(add_layernorm_kernel, H, grid, s, y, bias, x, g, b, rows_max, rows_dev, H, eps, x16);
     return hipGetLastError();
 }
 
 hipError_t launch_embed_ln(const int* tok_id, const int* tok_pos, const int* n_tokens,
                            int T_max, const float* word, const float* pos, const float* type0,
                            const float* g, const float* b, int V, int H, float eps, float* x,
-                           int* err, hipStream_t s) {
+                           int* err, uint16_t* x16, hipStream_t s) {
     if (T_max <= 0) return hipSuccess;
     const dim3 grid((T_max + 3) / 4);
     EBH_ROW_DISPATCH(embed_ln_kernel, H, grid, s, tok_id, tok_pos, n_tokens, word, pos, type0, g,
-                     b, V, H, eps, x, err);
+                     b, V, H, eps, x, err, x16);
     return hipGetLastError();
 }
 

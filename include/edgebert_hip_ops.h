@@ -37,6 +37,15 @@ EBH_API int ebh_op_gemm(const float* A, int64_t lda, const void* W, int64_t ldw,
                 const float* bias, const float* residual, int64_t ldr, float* C, int64_t ldc,
                 int32_t M, int32_t N, int32_t K, int32_t epilogue, void* stream);
 
+/* The same GEMM with bf16 activations: A [M, K] and W [N, K] bf16 bits, fp32
+ * accumulate, C [M, N] fp32 (c_dtype EBH_DTYPE_F32) or bf16 bits
+ * (EBH_DTYPE_BF16), epilogue EBH_EPI_BIAS / EBH_EPI_BIAS_GELU / EBH_EPI_NONE.
+ * K % 64 == 0, N % 4 == 0, strides of 8 / 8 / 4 elements, 16-byte aligned
+ * operands.  The forward of EBH_DTYPE_BF16 models uses it for every Linear. */
+EBH_API int ebh_op_gemm_bf16(const uint16_t* A, int64_t lda, const uint16_t* W, int64_t ldw,
+                     const float* bias, void* C, int64_t ldc, int32_t c_dtype, int32_t M, int32_t N,
+                     int32_t K, int32_t epilogue, void* stream);
+
 /* Masked multi-head attention (src/lib.rs:700-730 with 851-956) over packed
  * sequences: qkv [T, 3*hidden] rows (q | k | v), sequence b = rows
  * cu_seqlens[b] .. cu_seqlens[b+1]-1 (every row a real token, lengths <=

@@ -110,6 +110,33 @@ def test_gemm_bf16(env, M, N, K, epi):
     np.testing.assert_allclose(dC.cpu().numpy(), want, rtol=0, atol=2e-5 * np.sqrt(K))
 
 
+@pytest.mark.parametrize("M,N,K", [(5, 16, 64), (300, 2304, 768), (257, 768, 3072), (1000, 3072, 768),
+                                   (130, 100, 128)])
+@pytest.mark.parametrize("epi", [0, 1, 3])
+@pytest.mark.parametrize("c16", [False, True])
+def test_gemm_bf16_activations(env, M, N, K, epi, c16):
+    """bf16 A and W (the forward of bf16 models): equal to the float64 product of
+    the same bf16 values up to fp32 summation; a bf16 C is that, rounded."""
+    torch, eb, Nn, L = env
+    rng = np.random.default_rng(M + N + K + epi + int(c16))
+    A = torch.from_numpy(rng.standard_normal((M, K)).astype(np.float32)).to(torch.bfloat16)
+    W = torch.from_numpy((0.05 * rng.standard_normal((N, K))).astype(np.float32)).to(torch.bfloat16)
+    bias = rng.standard_normal(N).astype(np.float32)
+    dA, dW, db = A.cuda(), W.cuda(), dev(torch, bias)
+    dC = torch.full((M, N), float("nan"), device="cuda", dtype=torch.bfloat16 if c16 else torch.float32)
+    Nn.check(L.ebh_op_gemm_bf16(vp(dA), K, vp(dW), K, vp(db) if epi != 3 else None, vp(dC), N,
+                                Nn.EBH_DTYPE_BF16 if c16 else Nn.EBH_DTYPE_F32, M, N, K, epi, stream(torch)))
+    torch.cuda.synchronize()
+    want = A.double().numpy() @ W.double().numpy().T + (bias if epi != 3 else 0.0)
+    if epi == 1:
+        want = gelu64(want)
+    got = dC.float().cpu().numpy()
+    if c16:   # one bf16 rounding of the fp32 result (relative 2^-8)
+        np.testing.assert_allclose(got, want, rtol=2 ** -8, atol=1e-4 * np.sqrt(K))
+    else:
+        np.testing.assert_allclose(got, want, rtol=0, atol=2e-5 * np.sqrt(K))
+
+
 def test_f32_to_bf16_round_to_nearest_even(env):
     torch, eb, Nn, L = env
     rng = np.random.default_rng(3)
