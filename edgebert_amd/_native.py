@@ -66,6 +66,7 @@ _SIGS = {
     "ebh_op_gemm_bf16": (_i32, [_vp, _i64, _vp, _i64, _vp, _vp, _i64, _i32, _i32, _i32, _i32, _i32,
                                 _vp]),
     "ebh_op_attention": (_i32, [_vp, _vp, _i32, _i32, _i32, _i32, _vp, _vp]),
+    "ebh_op_attention_bf16": (_i32, [_vp, _vp, _i32, _i32, _i32, _i32, _vp, _vp]),
     "ebh_op_layer_norm": (_i32, [_vp, _vp, _vp, _i32, _i32, _f32, _vp, _vp]),
     "ebh_op_add_layer_norm": (_i32, [_vp, _vp, _vp, _vp, _vp, _i32, _i32, _f32, _vp]),
     "ebh_op_pool": (_i32, [_vp, _vp, _i32, _i32, _i32, _i32, _vp, _vp]),

@@ -286,8 +286,9 @@ int enqueue_forward(ebh_model* m, const int* d_ids, const int* d_mask, int B, in
 
     // bf16 models keep the residual stream X in fp32 (LayerNorm, softmax and
     // every sum stay fp32) and hand the GEMMs bf16 operands: X16 (written by
-    // each LayerNorm), the attention context and the GELU output, each stored
-    // as bf16 in the first half of its fp32 buffer.
+    // each LayerNorm), q / k / v, the attention context and the GELU output,
+    // each stored as bf16 in the first half of its fp32 buffer.
+    uint16_t* qkv16 = reinterpret_cast<uint16_t*>(w.QKV);
     uint16_t* ctx16 = reinterpret_cast<uint16_t*>(w.CTX);
     uint16_t* f16 = reinterpret_cast<uint16_t*>(w.F);
     auto gemm = [&](int kind, const void* A, int64_t lda, const float* W32, const uint16_t* W16,
@@ -321,11 +322,13 @@ int enqueue_forward(ebh_model* m, const int* d_ids, const int* d_mask, int B, in
     for (const DevLayer& L : m->layers) {
         int rc;
         if ((rc = gemm(EBH_PROF_GEMM_QKV, bf16 ? (const void*)w.X16 : w.X, H, L.wqkv, L.wqkv16, L.bqkv,
-                       w.QKV, 3 * H, H, ebh::EPI_BIAS, false)))
+                       bf16 ? (void*)qkv16 : (void*)w.QKV, 3 * H, H, ebh::EPI_BIAS, bf16)))
             return rc;
         prof_begin(m, EBH_PROF_ATTENTION, s, pp, on);
-        HIP_TRY(ebh::launch_attention(w.QKV, w.cu, B, S, H, nh, hd, scale,
-                                      bf16 ? (void*)ctx16 : (void*)w.CTX, bf16, s));
+        if (bf16)
+            HIP_TRY(ebh::launch_attention_bf16(qkv16, w.cu, B, S, H, nh, hd, scale, ctx16, s));
+        else
+            HIP_TRY(ebh::launch_attention(w.QKV, w.cu, B, S, H, nh, hd, scale, w.CTX, false, s));
         prof_end(m, s, pp, on);
         if ((rc = gemm(EBH_PROF_GEMM_OUT, bf16 ? (const void*)ctx16 : w.CTX, H, L.wo, L.wo16, nullptr,
                        w.Y, H, H, ebh::EPI_NONE, false)))
@@ -779,6 +782,22 @@ int ebh_op_attention(const float* qkv, const int32_t* cu_seqlens, int32_t B, int
     const float scale = 1.0f / sqrtf((float)hd);
     HIP_TRY(ebh::launch_attention(qkv, cu_seqlens, B, max_len, hidden, num_heads, hd, scale, ctx,
                                   false, static_cast<hipStream_t>(stream)));
+    return EBH_OK;
+}
+
+int ebh_op_attention_bf16(const uint16_t* qkv, const int32_t* cu_seqlens, int32_t B,
+                          int32_t max_len, int32_t hidden, int32_t num_heads, uint16_t* ctx,
+                          void* stream) {
+    if (!qkv || !cu_seqlens || !ctx) return fail(EBH_ERR_INVALID_ARG, "null buffer");
+    if (B < 0 || max_len < 0 || hidden <= 0 || num_heads <= 0 || hidden % num_heads)
+        return fail(EBH_ERR_INVALID_ARG, "bad attention shape");
+    const int hd = hidden / num_heads;
+    if (hd != 32 && hd != 64) return fail(EBH_ERR_INVALID_ARG, "head_dim %d unsupported", hd);
+    if (reinterpret_cast<uintptr_t>(qkv) % 16 || reinterpret_cast<uintptr_t>(ctx) % 2)
+        return fail(EBH_ERR_INVALID_ARG, "qkv must be 16-byte aligned");
+    const float scale = 1.0f / sqrtf((float)hd);
+    HIP_TRY(ebh::launch_attention_bf16(qkv, cu_seqlens, B, max_len, hidden, num_heads, hd, scale,
+                                       ctx, static_cast<hipStream_t>(stream)));
     return EBH_OK;
 }
 

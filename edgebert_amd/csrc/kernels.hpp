@@ -33,6 +33,12 @@ hipError_t launch_attention(const float* qkv, const int* cu_seqlens, int B, int 
                             int H, int nh, int head_dim, float scale, void* ctx, bool ctx_bf16,
                             hipStream_t s);
 
+// Attention with bf16 q / k / v (qkv [T, 3H] bf16 bits) and bf16 context;
+// scores, softmax and accumulation in fp32.  head_dim 32 or 64.
+hipError_t launch_attention_bf16(const uint16_t* qkv, const int* cu_seqlens, int B, int max_len,
+                                 int H, int nh, int head_dim, float scale, uint16_t* ctx,
+                                 hipStream_t s);
+
 // bf16 activations and weights, fp32 accumulate: C = epi(A . W^T + bias), A [M,K]
 // and W [N,K] bf16 bits, C fp32 or (c_bf16) bf16 bits.  Needs 16-byte aligned
 // operands and rows, N % 4 == 0 and K % 64 == 0 (hipErrorInvalidValue otherwise).

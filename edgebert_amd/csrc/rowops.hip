@@ -208,6 +208,145 @@ __global__ __launch_bounds__(256) void embed_ln_kernel(
     ln_row<NC>(v, lane, H, g, bta, eps, x + (int64_t)t * H, x16 ? x16 + (int64_t)t * H : nullptr);
 }
 
+// ---------------------------------------------------------------------------
+// float4 variants of the LayerNorm row kernels: LPR lanes per row (16, 32 or
+// 64, so one wave holds 64 / LPR rows), each lane NV float4 at elements
+// 4 * (c * LPR + sub) .. +3, H == 4 * NV * LPR.  Every global access is a
+// 16-byte lane access (a wave instruction moves 1 KB), the row stays in
+// registers, and mean / variance are reductions over the row's lane group.
+// ---------------------------------------------------------------------------
+template <int LPR>
+__device__ __forceinline__ float group_sum(float v) {
+#pragma unroll
+    for (int o = LPR / 2; o > 0; o >>= 1) v += __shfl_xor(v, o);
+    return v;
+}
+
+template <int NV, int LPR>
+__device__ __forceinline__ void ln_row4(float4 (&v)[NV], int sub, int H, const float* g,
+                                        const float* b, float eps, float* y, uint16_t* y16) {
+    float s = 0.0f;
+#pragma unroll
+    for (int c = 0; c < NV; ++c) s += (v[c].x + v[c].y) + (v[c].z + v[c].w);
+    const float mean = group_sum<LPR>(s) / (float)H;
+    float ss = 0.0f;
+#pragma unroll
+    for (int c = 0; c < NV; ++c) {
+        const float dx = v[c].x - mean, dy = v[c].y - mean, dz = v[c].z - mean, dw = v[c].w - mean;
+        ss += (dx * dx + dy * dy) + (dz * dz + dw * dw);
+    }
+    const float var = group_sum<LPR>(ss) / (float)H;
+    const float inv_std = 1.0f / sqrtf(var + eps);
+#pragma unroll
+    for (int c = 0; c < NV; ++c) {
+        const int i = 4 * (c * LPR + sub);
+        const float4 g4 = *reinterpret_cast<const float4*>(g + i);
+        const float4 b4 = *reinterpret_cast<const float4*>(b + i);
+        float4 o;
+        o.x = (v[c].x - mean) * inv_std * g4.x + b4.x;
+        o.y = (v[c].y - mean) * inv_std * g4.y + b4.y;
+        o.z = (v[c].z - mean) * inv_std * g4.z + b4.z;
+        o.w = (v[c].w - mean) * inv_std * g4.w + b4.w;
+        *reinterpret_cast<float4*>(y + i) = o;
+        if (y16) {
+            uint2 h;
+            h.x = (uint32_t)f32_to_bf16_rne(o.x) | ((uint32_t)f32_to_bf16_rne(o.y) << 16);
+            h.y = (uint32_t)f32_to_bf16_rne(o.z) | ((uint32_t)f32_to_bf16_rne(o.w) << 16);
+            *reinterpret_cast<uint2*>(y16 + i) = h;
+        }
+    }
+}
+
+template <int NV, int LPR>
+__global__ __launch_bounds__(256) void add_layernorm4_kernel(const float* __restrict__ y,
+                                                             const float* __restrict__ bias,
+                                                             float* x, const float* __restrict__ g,
+                                                             const float* __restrict__ bta,
+                                                             int rows_max, const int* rows_dev,
+                                                             int H, float eps, uint16_t* x16) {
+    constexpr int RPB = 256 / LPR;                // rows per workgroup
+    const int row = blockIdx.x * RPB + threadIdx.x / LPR, sub = threadIdx.x % LPR;
+    const int rows = rows_dev ? *rows_dev : rows_max;
+    if (row >= rows) return;
+    const float* yr = y + (int64_t)row * H;
+    float* xr = x + (int64_t)row * H;
+    float4 v[NV];
+#pragma unroll
+    for (int c = 0; c < NV; ++c) {
+        const int i = 4 * (c * LPR + sub);
+        const float4 a = *reinterpret_cast<const float4*>(yr + i);
+        const float4 bb = *reinterpret_cast<const float4*>(bias + i);
+        const float4 r = *reinterpret_cast<const float4*>(xr + i);
+        v[c] = make_float4((a.x + bb.x) + r.x, (a.y + bb.y) + r.y, (a.z + bb.z) + r.z, (a.w + bb.w) + r.w);
+    }
+    ln_row4<NV, LPR>(v, sub, H, g, bta, eps, xr, x16 ? x16 + (int64_t)row * H : nullptr);
+}
+
+template <int NV, int LPR>
+__global__ __launch_bounds__(256) void embed_ln4_kernel(
+    const int* __restrict__ tok_id, const int* __restrict__ tok_pos,
+    const int* __restrict__ n_tokens, const float* __restrict__ word,
+    const float* __restrict__ pos, const float* __restrict__ type0, const float* __restrict__ g,
+    const float* __restrict__ bta, int V, int H, float eps, float* __restrict__ x,
+    int* __restrict__ err, uint16_t* __restrict__ x16) {
+    constexpr int RPB = 256 / LPR;
+    const int t = blockIdx.x * RPB + threadIdx.x / LPR, sub = threadIdx.x % LPR;
+    if (t >= *n_tokens) return;
+    int id = tok_id[t];
+    if (id < 0 || id >= V) {
+        if (sub == 0) atomicOr(err, 1);
+        id = 0;
+    }
+    const float* wr = word + (int64_t)id * H;
+    const float* pr = pos + (int64_t)tok_pos[t] * H;
+    float4 v[NV];
+#pragma unroll
+    for (int c = 0; c < NV; ++c) {
+        const int i = 4 * (c * LPR + sub);
+        const float4 a = *reinterpret_cast<const float4*>(wr + i);
+        const float4 p4 = *reinterpret_cast<const float4*>(pr + i);
+        const float4 ty = *reinterpret_cast<const float4*>(type0 + i);
+        v[c] = make_float4((a.x + p4.x) + ty.x, (a.y + p4.y) + ty.y, (a.z + p4.z) + ty.z, (a.w + p4.w) + ty.w);
+    }
+    ln_row4<NV, LPR>(v, sub, H, g, bta, eps, x + (int64_t)t * H, x16 ? x16 + (int64_t)t * H : nullptr);
+}
+
+// (LPR, NV) for a row of H floats, or LPR = 0 when the float4 kernels do not apply.
+static void row4_shape(int H, int& lpr, int& nv) {
+    lpr = 0;
+    nv = 0;
+    const int cands[3] = {64, 32, 16};
+    for (int c : cands)
+        if (H % (4 * c) == 0) {
+            const int n = H / (4 * c);
+            if (n == 1 || n == 2 || n == 3 || n == 4 || n == 6 || n == 8) { lpr = c; nv = n; return; }
+        }
+}
+
+#define EBH_ROW4_DISPATCH(KERNEL, LPR, NV, GRIDF, STREAM, ...)                                 \
+    do {                                                                                         \
+        bool done_ = false;                                                                      \
+        EBH_ROW4_L(KERNEL, 64, LPR, NV, GRIDF, STREAM, __VA_ARGS__)                              \
+        EBH_ROW4_L(KERNEL, 32, LPR, NV, GRIDF, STREAM, __VA_ARGS__)                              \
+        EBH_ROW4_L(KERNEL, 16, LPR, NV, GRIDF, STREAM, __VA_ARGS__)                              \
+        if (!done_) return hipErrorInvalidValue;                                                 \
+    } while (0)
+#define EBH_ROW4_L(KERNEL, L, LPR, NV, GRIDF, STREAM, ...)                                      \
+    if (LPR == L) {                                                                              \
+        const dim3 grid_((GRIDF + 256 / L - 1) / (256 / L));                                     \
+        switch (NV) {                                                                            \
+            case 1: hipLaunchKernelGGL((KERNEL<1, L>), grid_, dim3(256), 0, STREAM, __VA_ARGS__); done_ = true; break; \
+            case 2: hipLaunchKernelGGL((KERNEL<2, L>), grid_, dim3(256), 0, STREAM, __VA_ARGS__); done_ = true; break; \
+            case 3: hipLaunchKernelGGL((KERNEL<3, L>), grid_, dim3(256), 0, STREAM, __VA_ARGS__); done_ = true; break; \
+            case 4: hipLaunchKernelGGL((KERNEL<4, L>), grid_, dim3(256), 0, STREAM, __VA_ARGS__); done_ = true; break; \
+            case 6: hipLaunchKernelGGL((KERNEL<6, L>), grid_, dim3(256), 0, STREAM, __VA_ARGS__); done_ = true; break; \
+            case 8: hipLaunchKernelGGL((KERNEL<8, L>), grid_, dim3(256), 0, STREAM, __VA_ARGS__); done_ = true; break; \
+            default: break;                                                                      \
+        }                                                                                        \
+    }
+
+static bool al16(const void* p) { return ((uintptr_t)p & 15) == 0; }
+
 #define EBH_ROW_DISPATCH(KERNEL, H, GRID, STREAM, ...)                                       \
     do {                                                                                     \
         const int nc_ = ((H) + 63) / 64;                                                     \
@@ -232,6 +371,13 @@ hipError_t launch_add_layernorm(const float* y, const float* bias, float* x, con
                                 const float* b, int rows_max, const int* rows_dev, int H, float eps,
                                 uint16_t* x16, hipStream_t s) {
     if (rows_max <= 0) return hipSuccess;
+    int lpr, nv;
+    row4_shape(H, lpr, nv);
+    if (lpr && al16(y) && al16(bias) && al16(x) && al16(g) && al16(b) && (!x16 || ((uintptr_t)x16 & 7) == 0)) {
+        EBH_ROW4_DISPATCH(add_layernorm4_kernel, lpr, nv, rows_max, s, y, bias, x, g, b, rows_max,
+                          rows_dev, H, eps, x16);
+        return hipGetLastError();
+    }
     const dim3 grid((rows_max + 3) / 4);
     EBH_ROW_DISPATCH(add_layernorm_kernel, H, grid, s, y, bias, x, g, b, rows_max, rows_dev, H, eps, x16);
     return hipGetLastError();
@@ -242,6 +388,14 @@ hipError_t launch_embed_ln(const int* tok_id, const int* tok_pos, const int* n_t
                            const float* g, const float* b, int V, int H, float eps, float* x,
                            int* err, uint16_t* x16, hipStream_t s) {
     if (T_max <= 0) return hipSuccess;
+    int lpr, nv;
+    row4_shape(H, lpr, nv);
+    if (lpr && al16(word) && al16(pos) && al16(type0) && al16(g) && al16(b) && al16(x) &&
+        (!x16 || ((uintptr_t)x16 & 7) == 0)) {
+        EBH_ROW4_DISPATCH(embed_ln4_kernel, lpr, nv, T_max, s, tok_id, tok_pos, n_tokens, word, pos,
+                          type0, g, b, V, H, eps, x, err, x16);
+        return hipGetLastError();
+    }
     const dim3 grid((T_max + 3) / 4);
     EBH_ROW_DISPATCH(embed_ln_kernel, H, grid, s, tok_id, tok_pos, n_tokens, word, pos, type0, g,
                      b, V, H, eps, x, err, x16);

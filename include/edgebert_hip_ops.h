@@ -54,6 +54,14 @@ EBH_API int ebh_op_gemm_bf16(const uint16_t* A, int64_t lda, const uint16_t* W, 
 EBH_API int ebh_op_attention(const float* qkv, const int32_t* cu_seqlens, int32_t B, int32_t max_len,
                      int32_t hidden, int32_t num_heads, float* ctx, void* stream);
 
+/* The same attention for bf16 models: qkv [T, 3*hidden] and ctx [T, hidden]
+ * hold bf16 bit patterns (qkv 16-byte aligned); q.k^T, softmax and the P.V
+ * sums accumulate in fp32 (bf16 counterpart of the reference's fp32
+ * attention, src/lib.rs:700-730). */
+EBH_API int ebh_op_attention_bf16(const uint16_t* qkv, const int32_t* cu_seqlens, int32_t B,
+                          int32_t max_len, int32_t hidden, int32_t num_heads, uint16_t* ctx,
+                          void* stream);
+
 /* apply_layer_norm_3d (src/lib.rs:980-991) over rows x [rows, H] -> y (may alias). */
 EBH_API int ebh_op_layer_norm(const float* x, const float* gamma, const float* beta, int32_t rows,
                       int32_t H, float eps, float* y, void* stream);

@@ -194,6 +194,31 @@ def test_attention(env, H, nh, lengths):
     np.testing.assert_allclose(dctx.cpu().numpy(), attention64(qkv, cu, H, nh), rtol=0, atol=2e-5)
 
 
+@pytest.mark.parametrize("H,nh,lengths", [
+    (384, 12, [1, 2, 31, 32, 33, 127, 128, 129]),
+    (384, 12, [256, 300, 511, 512]),
+    (768, 12, [1, 64, 128, 130, 257]),
+    (64, 2, [5, 17]),
+])
+def test_attention_bf16(env, H, nh, lengths):
+    """bf16 q / k / v and context: the float64 attention of the same bf16 values,
+    within the bf16 rounding of the probabilities and of the result."""
+    torch, eb, Nn, L = env
+    rng = np.random.default_rng(sum(lengths) + H + 1)
+    T = sum(lengths)
+    qkv = torch.from_numpy(rng.standard_normal((T, 3 * H)).astype(np.float32)).to(torch.bfloat16)
+    cu = np.concatenate([[0], np.cumsum(lengths)]).astype(np.int32)
+    dq, dcu = qkv.cuda(), dev(torch, cu)
+    dctx = torch.full((T, H), float("nan"), device="cuda", dtype=torch.bfloat16)
+    Nn.check(L.ebh_op_attention_bf16(vp(dq), vp(dcu), len(lengths), max(lengths), H, nh, vp(dctx),
+                                     stream(torch)))
+    torch.cuda.synchronize()
+    want = attention64(qkv.float().numpy(), cu, H, nh)
+    # |ctx| <= max|v| ~ 4; probabilities carry 2^-9 relative error, the output one
+    # more bf16 rounding.
+    np.testing.assert_allclose(dctx.float().cpu().numpy(), want, rtol=2 ** -8, atol=1e-2)
+
+
 def test_attention_empty_sequence_writes_nothing(env):
     torch, eb, Nn, L = env
     H, nh = 384, 12
