@@ -866,24 +866,21 @@ hipError_t launch_gemm_f32(const GemmArgs& a, int epi, hipStream_t s) {
     const bool ok = epi != EPI_BIAS_RESID && aligned16(a.A) && aligned16(a.W) && aligned16(a.C) &&
                     (epi == EPI_NONE || aligned16(a.bias)) && a.lda % 4 == 0 && a.ldw % 4 == 0 &&
                     a.ldc % 4 == 0 && a.N % 4 == 0;
-    // Tile choice measured on MI355X at MiniLM shapes.  Many tokens (M = 32768):
-    // 64-deep k-tiles with two LDS stages and one workgroup per CU; 8 waves for
-    // narrow outputs, 4 for wide; for wide outputs over a short K (FFN up, at
-    // least 8 tiles per CU) 32-deep k-tiles and two workgroups per CU, so one
-    // workgroup's epilogue runs beside the other's MFMAs.
-    // Few tokens (under half a 128 x 128 tile per CU, e.g. the narrow
-    // projections of batch 32 of short sentences): 64 x 64 tiles, two
-    // workgroups per CU, so that most CUs have work and their SIMDs have a
-    // second wave to switch to.
+    // Tile choice measured on MI355X at MiniLM shapes (M = 2.4k .. 32k tokens):
+    //  * few tokens (under half a 128 x 128 tile per CU, e.g. the narrow
+    //    projections of batch 32 of short sentences): 64 x 64 tiles, two
+    //    workgroups per CU, so most CUs have work and their SIMDs a second wave;
+    //  * wide outputs over a short K with many tiles per CU (FFN up at 32k
+    //    tokens): 32-deep k-tiles, two workgroups per CU, so one workgroup's
+    //    GELU epilogue runs beside the other's MFMAs;
+    //  * otherwise 128 x 128 tiles, 64-deep k-tiles, 8 waves (two per SIMD).
     const int64_t tiles128 = (int64_t)((a.M_max + 127) / 128) * ((a.N + 127) / 128);
     if (ok && a.K % 64 == 0 && 2 * tiles128 < (int64_t)cu_count())
         return launch_persistent<64, 64, 64, 2, 2, 2>(a, epi, s, 2);
     if (ok && a.K % 32 == 0 && a.N >= 1536 && a.K < 1024 && tiles128 >= 8 * (int64_t)cu_count())
         return launch_persistent<128, 128, 32, 2, 2, 2>(a, epi, s, 2);
-    if (ok && a.K % 64 == 0 && a.N <= 512)
-        return launch_persistent<128, 128, 64, 2, 4, 2>(a, epi, s, 1);
     if (ok && a.K % 64 == 0)
-        return launch_persistent<128, 128, 64, 2, 2, 2>(a, epi, s, 1);
+        return launch_persistent<128, 128, 64, 2, 4, 2>(a, epi, s, 1);
     if (ok && a.K % 32 == 0)
         return launch_persistent<128, 128, 32, 2, 2, 2>(a, epi, s, 2);
     return launch_tile<128, 128, 32, 2, 2, false>(a, epi, s);

@@ -79,6 +79,32 @@ def test_gemm_f32(env, M, N, K, epi):
     np.testing.assert_allclose(got, want, rtol=0, atol=tol)
 
 
+@pytest.mark.parametrize("M,N,K,epi", [
+    (4100, 1152, 384, 0),      # 128 x 128 tiles, 8 waves (row tail of 4)
+    (8192, 384, 1536, 3),      # 8 waves, long K, no bias
+    (33000, 1536, 384, 1),     # many tiles per CU: 32-deep k-tiles, two workgroups per CU
+    (500, 256, 96, 0),         # K % 64 != 0: 32-deep k-tiles
+])
+def test_gemm_f32_dispatch_paths(env, M, N, K, epi):
+    """The tile configurations chosen for many tokens, each against the float64
+    product (the small shapes above all take the few-token or guarded kernels)."""
+    torch, eb, Nn, L = env
+    rng = np.random.default_rng(M + N + K)
+    A = rng.standard_normal((M, K)).astype(np.float32)
+    W = (0.05 * rng.standard_normal((N, K))).astype(np.float32)
+    bias = rng.standard_normal(N).astype(np.float32)
+    dA, dW, db = dev(torch, A), dev(torch, W), dev(torch, bias)
+    dC = torch.full((M, N), float("nan"), device="cuda")
+    Nn.check(L.ebh_op_gemm(vp(dA), K, vp(dW), K, Nn.EBH_DTYPE_F32, vp(db) if epi != 3 else None,
+                           None, N, vp(dC), N, M, N, K, epi, stream(torch)))
+    torch.cuda.synchronize()
+    want = A.astype(np.float64) @ W.T.astype(np.float64) + (bias if epi != 3 else 0.0)
+    if epi == 1:
+        want = gelu64(want)
+    tol = 2e-6 * np.sqrt(K) * (np.abs(A).max() * np.abs(W).max() * np.sqrt(K)) + 1e-5
+    np.testing.assert_allclose(dC.cpu().numpy(), want, rtol=0, atol=tol)
+
+
 def _bf16_round(x):
     import torch
     return torch.from_numpy(np.ascontiguousarray(x, np.float32)).to(torch.bfloat16).float().numpy()
