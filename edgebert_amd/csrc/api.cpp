@@ -317,8 +317,14 @@ int enqueue_forward(ebh_model* m, const int* d_ids, const int* d_mask, int B, in
     };
 
     // Per layer (BertLayer::forward, src/lib.rs:669-683): the attention-output and
-    // FFN-down projections are written without bias; their bias and the block's
-    // residual are added, in the reference's order, by the LayerNorm that follows.
+    // FFN-down projections are written without bias (as bf16 in bf16 models);
+    // their bias and the block's residual are added in fp32, in the reference's
+    // order, by the LayerNorm that follows.
+    auto add_ln = [&](const float* bias, const float* g, const float* b) -> hipError_t {
+        return bf16 ? ebh::launch_add_layernorm_y16(reinterpret_cast<const uint16_t*>(w.Y), bias, w.X, g, b, T,
+                                                    w.ntok, H, eps, w.X16, s)
+                    : ebh::launch_add_layernorm(w.Y, bias, w.X, g, b, T, w.ntok, H, eps, w.X16, s);
+    };
     for (const DevLayer& L : m->layers) {
         int rc;
         if ((rc = gemm(EBH_PROF_GEMM_QKV, bf16 ? (const void*)w.X16 : w.X, H, L.wqkv, L.wqkv16, L.bqkv,
@@ -331,19 +337,19 @@ int enqueue_forward(ebh_model* m, const int* d_ids, const int* d_mask, int B, in
             HIP_TRY(ebh::launch_attention(w.QKV, w.cu, B, S, H, nh, hd, scale, w.CTX, false, s));
         prof_end(m, s, pp, on);
         if ((rc = gemm(EBH_PROF_GEMM_OUT, bf16 ? (const void*)ctx16 : w.CTX, H, L.wo, L.wo16, nullptr,
-                       w.Y, H, H, ebh::EPI_NONE, false)))
+                       w.Y, H, H, ebh::EPI_NONE, bf16)))
             return rc;
         prof_begin(m, EBH_PROF_LAYERNORM, s, pp, on);
-        HIP_TRY(ebh::launch_add_layernorm(w.Y, L.bo, w.X, L.ln1_g, L.ln1_b, T, w.ntok, H, eps, w.X16, s));
+        HIP_TRY(add_ln(L.bo, L.ln1_g, L.ln1_b));
         prof_end(m, s, pp, on);
         if ((rc = gemm(EBH_PROF_GEMM_FFN_UP, bf16 ? (const void*)w.X16 : w.X, H, L.w1, L.w116, L.b1,
                        bf16 ? (void*)f16 : (void*)w.F, I, H, ebh::EPI_BIAS_GELU, bf16)))
             return rc;
         if ((rc = gemm(EBH_PROF_GEMM_FFN_DOWN, bf16 ? (const void*)f16 : w.F, I, L.w2, L.w216, nullptr,
-                       w.Y, H, I, ebh::EPI_NONE, false)))
+                       w.Y, H, I, ebh::EPI_NONE, bf16)))
             return rc;
         prof_begin(m, EBH_PROF_LAYERNORM, s, pp, on);
-        HIP_TRY(ebh::launch_add_layernorm(w.Y, L.b2, w.X, L.ln2_g, L.ln2_b, T, w.ntok, H, eps, w.X16, s));
+        HIP_TRY(add_ln(L.b2, L.ln2_g, L.ln2_b));
         prof_end(m, s, pp, on);
     }
     prof_begin(m, EBH_PROF_POOL, s, pp, on);
@@ -437,8 +443,11 @@ int ebh_finalize(ebh_model* m, int32_t dtype) {
     if (m->finalized) return fail(EBH_ERR_STATE, "model already finalized");
     if (dtype != EBH_DTYPE_F32 && dtype != EBH_DTYPE_BF16)
         return fail(EBH_ERR_INVALID_ARG, "unknown dtype %d", dtype);
-    if (dtype == EBH_DTYPE_BF16 && (m->cfg.hidden_size % 64 || m->cfg.intermediate_size % 64))
-        return fail(EBH_ERR_INVALID_ARG, "bf16 models need hidden_size and intermediate_size multiples of 64");
+    if (dtype == EBH_DTYPE_BF16 && (m->cfg.hidden_size % 64 || m->cfg.intermediate_size % 64 ||
+                                    !ebh::row4_shape_ok(m->cfg.hidden_size)))
+        return fail(EBH_ERR_INVALID_ARG,
+                    "bf16 models need hidden_size and intermediate_size multiples of 64, and hidden_size "
+                    "= 4 * L * n with L in {64, 32, 16} and n in {1, 2, 3, 4, 6, 8}");
     const auto names = expected_tensors(m->cfg);
     for (auto& kv : names)
         if (!m->host.count(kv.first)) return fail(EBH_ERR_NOT_FOUND, "Tensor %s not found", kv.first.c_str());
@@ -816,6 +825,15 @@ int ebh_op_add_layer_norm(const float* y, const float* bias, float* x, const flo
     if (rows < 0 || H <= 0 || H > 2048) return fail(EBH_ERR_INVALID_ARG, "bad LayerNorm shape");
     HIP_TRY(ebh::launch_add_layernorm(y, bias, x, gamma, beta, rows, nullptr, H, eps, nullptr,
                                       static_cast<hipStream_t>(stream)));
+    return EBH_OK;
+}
+
+int ebh_op_add_layer_norm_y16(const uint16_t* y, const float* bias, float* x, const float* gamma,
+                              const float* beta, int32_t rows, int32_t H, float eps, void* stream) {
+    if (!y || !bias || !x || !gamma || !beta) return fail(EBH_ERR_INVALID_ARG, "null buffer");
+    if (rows < 0 || H <= 0 || !ebh::row4_shape_ok(H)) return fail(EBH_ERR_INVALID_ARG, "bad LayerNorm shape");
+    HIP_TRY(ebh::launch_add_layernorm_y16(y, bias, x, gamma, beta, rows, nullptr, H, eps, nullptr,
+                                          static_cast<hipStream_t>(stream)));
     return EBH_OK;
 }
 

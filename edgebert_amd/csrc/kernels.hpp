@@ -53,6 +53,14 @@ hipError_t launch_layernorm(const float* x, float* y, const float* g, const floa
 hipError_t launch_add_layernorm(const float* y, const float* bias, float* x, const float* g,
                                 const float* b, int rows_max, const int* rows_dev, int H, float eps,
                                 uint16_t* x16, hipStream_t s);
+// The same with y stored as bf16 (bf16 models).  Needs 8-byte aligned bf16
+// rows, 16-byte aligned fp32 operands and row4_shape_ok(H).
+// H = 4 * L * n with L lanes per row in {64, 32, 16} and n float4 per lane in
+// {1, 2, 3, 4, 6, 8}: the shapes the float4 row kernels take.
+bool row4_shape_ok(int H);
+hipError_t launch_add_layernorm_y16(const uint16_t* y, const float* bias, float* x, const float* g,
+                                    const float* b, int rows_max, const int* rows_dev, int H, float eps,
+                                    uint16_t* x16, hipStream_t s);
 
 // Token packing: mask [B,S] -> cu_seqlens [B+1], n_tokens, packed ids/positions.
 hipError_t launch_pack(const int* ids, const int* mask, int B, int S, int* counts, int* cu,

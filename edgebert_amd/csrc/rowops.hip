@@ -282,6 +282,36 @@ __global__ __launch_bounds__(256) void add_layernorm4_kernel(const float* __rest
     ln_row4<NV, LPR>(v, sub, H, g, bta, eps, xr, x16 ? x16 + (int64_t)row * H : nullptr);
 }
 
+// The same with the projection y stored as bf16 (bf16 models write the
+// attention-output and FFN-down products in bf16); the sum, statistics and
+// output stay fp32.
+template <int NV, int LPR>
+__global__ __launch_bounds__(256) void add_layernorm4_y16_kernel(const uint16_t* __restrict__ y,
+                                                                 const float* __restrict__ bias,
+                                                                 float* x, const float* __restrict__ g,
+                                                                 const float* __restrict__ bta,
+                                                                 int rows_max, const int* rows_dev,
+                                                                 int H, float eps, uint16_t* x16) {
+    constexpr int RPB = 256 / LPR;
+    const int row = blockIdx.x * RPB + threadIdx.x / LPR, sub = threadIdx.x % LPR;
+    const int rows = rows_dev ? *rows_dev : rows_max;
+    if (row >= rows) return;
+    const uint16_t* yr = y + (int64_t)row * H;
+    float* xr = x + (int64_t)row * H;
+    float4 v[NV];
+#pragma unroll
+    for (int c = 0; c < NV; ++c) {
+        const int i = 4 * (c * LPR + sub);
+        const uint2 a = *reinterpret_cast<const uint2*>(yr + i);
+        const float4 bb = *reinterpret_cast<const float4*>(bias + i);
+        const float4 r = *reinterpret_cast<const float4*>(xr + i);
+        const float a0 = __uint_as_float(a.x << 16), a1 = __uint_as_float(a.x & 0xFFFF0000u);
+        const float a2 = __uint_as_float(a.y << 16), a3 = __uint_as_float(a.y & 0xFFFF0000u);
+        v[c] = make_float4((a0 + bb.x) + r.x, (a1 + bb.y) + r.y, (a2 + bb.z) + r.z, (a3 + bb.w) + r.w);
+    }
+    ln_row4<NV, LPR>(v, sub, H, g, bta, eps, xr, x16 ? x16 + (int64_t)row * H : nullptr);
+}
+
 template <int NV, int LPR>
 __global__ __launch_bounds__(256) void embed_ln4_kernel(
     const int* __restrict__ tok_id, const int* __restrict__ tok_pos,
@@ -321,6 +351,12 @@ static void row4_shape(int H, int& lpr, int& nv) {
             const int n = H / (4 * c);
             if (n == 1 || n == 2 || n == 3 || n == 4 || n == 6 || n == 8) { lpr = c; nv = n; return; }
         }
+}
+
+bool row4_shape_ok(int H) {
+    int lpr, nv;
+    row4_shape(H, lpr, nv);
+    return lpr != 0;
 }
 
 #define EBH_ROW4_DISPATCH(KERNEL, LPR, NV, GRIDF, STREAM, ...)                                 \
@@ -380,6 +416,20 @@ hipError_t launch_add_layernorm(const float* y, const float* bias, float* x, con
     }
     const dim3 grid((rows_max + 3) / 4);
     EBH_ROW_DISPATCH(add_layernorm_kernel, H, grid, s, y, bias, x, g, b, rows_max, rows_dev, H, eps, x16);
+    return hipGetLastError();
+}
+
+hipError_t launch_add_layernorm_y16(const uint16_t* y, const float* bias, float* x, const float* g,
+                                    const float* b, int rows_max, const int* rows_dev, int H, float eps,
+                                    uint16_t* x16, hipStream_t s) {
+    if (rows_max <= 0) return hipSuccess;
+    int lpr, nv;
+    row4_shape(H, lpr, nv);
+    if (!lpr || ((uintptr_t)y & 7) || !al16(bias) || !al16(x) || !al16(g) || !al16(b) ||
+        (x16 && ((uintptr_t)x16 & 7)))
+        return hipErrorInvalidValue;
+    EBH_ROW4_DISPATCH(add_layernorm4_y16_kernel, lpr, nv, rows_max, s, y, bias, x, g, b, rows_max,
+                      rows_dev, H, eps, x16);
     return hipGetLastError();
 }
 

@@ -72,6 +72,13 @@ EBH_API int ebh_op_layer_norm(const float* x, const float* gamma, const float* b
 EBH_API int ebh_op_add_layer_norm(const float* y, const float* bias, float* x, const float* gamma,
                           const float* beta, int32_t rows, int32_t H, float eps, void* stream);
 
+/* The same with y stored as bf16 (the projections of bf16 models); the sums,
+ * statistics and x stay fp32.  y rows 8-byte aligned, the fp32 operands
+ * 16-byte aligned, and H = 4 * L * n with L in {64, 32, 16}, n in
+ * {1, 2, 3, 4, 6, 8} (384, 768, 1024, ...). */
+EBH_API int ebh_op_add_layer_norm_y16(const uint16_t* y, const float* bias, float* x, const float* gamma,
+                              const float* beta, int32_t rows, int32_t H, float eps, void* stream);
+
 /* mean_pool (src/lib.rs:993-1010) over packed sequences (+ the normalise tail,
  * src/lib.rs:605-612, when normalize != 0); S is the padded length the caller
  * had (S > 0 and an empty sequence gives NaN, as in the reference). */

@@ -301,6 +301,30 @@ def test_add_layer_norm(env, H):
     np.testing.assert_allclose(dx.cpu().numpy(), want, rtol=0, atol=1e-5)
 
 
+@pytest.mark.parametrize("H", [384, 768])
+def test_add_layer_norm_bf16_projection(env, H):
+    """The same block end with y held as bf16 (bf16 models): equal to the fp32
+    kernel on the bf16 values of y; the error path rejects an unsupported H."""
+    torch, eb, Nn, L = env
+    import oracle
+    rng = np.random.default_rng(H + 2)
+    rows = 517
+    y16 = torch.from_numpy(rng.standard_normal((rows, H)).astype(np.float32)).to(torch.bfloat16)
+    x = rng.standard_normal((rows, H)).astype(np.float32)
+    b = rng.standard_normal(H).astype(np.float32)
+    g = rng.standard_normal(H).astype(np.float32)
+    beta = rng.standard_normal(H).astype(np.float32)
+    dy, dx, db, dg, dbeta = y16.cuda(), dev(torch, x), dev(torch, b), dev(torch, g), dev(torch, beta)
+    Nn.check(L.ebh_op_add_layer_norm_y16(vp(dy), vp(db), vp(dx), vp(dg), vp(dbeta), rows, H,
+                                         ctypes.c_float(1e-12), stream(torch)))
+    torch.cuda.synchronize()
+    y = y16.float().numpy()
+    want = oracle.layer_norm(((y + b) + x).astype(np.float32), g, beta, 1e-12)
+    np.testing.assert_allclose(dx.cpu().numpy(), want, rtol=0, atol=1e-5)
+    assert L.ebh_op_add_layer_norm_y16(vp(dy), vp(db), vp(dx), vp(dg), vp(dbeta), rows, 100,
+                                       ctypes.c_float(1e-12), stream(torch)) == Nn.EBH_ERR_INVALID_ARG
+
+
 @pytest.mark.parametrize("normalize", [0, 1])
 def test_pool(env, normalize):
     torch, eb, Nn, L = env
