@@ -788,6 +788,8 @@ int ebh_op_attention(const float* qkv, const int32_t* cu_seqlens, int32_t B, int
         return fail(EBH_ERR_INVALID_ARG, "bad attention shape");
     const int hd = hidden / num_heads;
     if (hd != 32 && hd != 64) return fail(EBH_ERR_INVALID_ARG, "head_dim %d unsupported", hd);
+    if (reinterpret_cast<uintptr_t>(qkv) % 16 || reinterpret_cast<uintptr_t>(ctx) % 16)
+        return fail(EBH_ERR_INVALID_ARG, "qkv and ctx must be 16-byte aligned");
     const float scale = 1.0f / sqrtf((float)hd);
     HIP_TRY(ebh::launch_attention(qkv, cu_seqlens, B, max_len, hidden, num_heads, hd, scale, ctx,
                                   false, static_cast<hipStream_t>(stream)));
@@ -802,8 +804,8 @@ int ebh_op_attention_bf16(const uint16_t* qkv, const int32_t* cu_seqlens, int32_
         return fail(EBH_ERR_INVALID_ARG, "bad attention shape");
     const int hd = hidden / num_heads;
     if (hd != 32 && hd != 64) return fail(EBH_ERR_INVALID_ARG, "head_dim %d unsupported", hd);
-    if (reinterpret_cast<uintptr_t>(qkv) % 16 || reinterpret_cast<uintptr_t>(ctx) % 2)
-        return fail(EBH_ERR_INVALID_ARG, "qkv must be 16-byte aligned");
+    if (reinterpret_cast<uintptr_t>(qkv) % 16 || reinterpret_cast<uintptr_t>(ctx) % 8)
+        return fail(EBH_ERR_INVALID_ARG, "qkv must be 16-byte and ctx 8-byte aligned");
     const float scale = 1.0f / sqrtf((float)hd);
     HIP_TRY(ebh::launch_attention_bf16(qkv, cu_seqlens, B, max_len, hidden, num_heads, hd, scale,
                                        ctx, static_cast<hipStream_t>(stream)));

@@ -17,9 +17,12 @@
 // v_mfma_f32_32x32x2_f32, so lane l owns query l%32 and, for each 32-key
 // block, keys 8*(r/4) + 4*(l/32) + r%4 (r = 0..15).  Row max / sum are then
 // per-lane reductions plus one exchange with lane l^32, and the
-// probabilities already sit in the A-operand layout of the P.V MFMA
-// (row = query = l%32, k = one key per lane half), so P never leaves
-// registers.
+// probabilities already sit in an operand layout of the P.V MFMA (query =
+// l%32, one key per lane half), so P never leaves registers.  The context is
+// accumulated transposed too, O^T = V^T . P^T: lane l then holds dims
+// 8*(r/4) + 4*(l/32) + r%4 of its own query l%32, so the online-softmax
+// rescale and the final division use the lane's own statistics, and the
+// context leaves as 16-byte stores of four consecutive dims.
 #include "kernels.hpp"
 
 namespace ebh {
@@ -128,13 +131,12 @@ __global__ __launch_bounds__(256) void attention_kernel(const float* __restrict_
         m_run = m_new;
         if (c > 0) {
 #pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const float ar = __shfl(alpha, 8 * (r >> 2) + 4 * half + (r & 3));
+            for (int j = 0; j < NJ; ++j)
 #pragma unroll
-                for (int j = 0; j < NJ; ++j) o[j][r] *= ar;
-            }
+                for (int r = 0; r < 16; ++r) o[j][r] *= alpha;
         }
-        // context += P . V over this chunk
+        // context^T += V^T . P^T over this chunk: A = V^T (row = dim l32, one
+        // key per lane half), B = P^T (that key, column = query l32).
 #pragma unroll
         for (int kb = 0; kb < 4; ++kb) {
             if (kb < nkb) {
@@ -144,29 +146,35 @@ __global__ __launch_bounds__(256) void attention_kernel(const float* __restrict_
 #pragma unroll
                     for (int j = 0; j < NJ; ++j)
                         o[j] = __builtin_amdgcn_mfma_f32_32x32x2f32(
-                            sc[kb][r], Vs[key * HD + j * 32 + l32], o[j], 0, 0, 0);
+                            Vs[key * HD + j * 32 + l32], sc[kb][r], o[j], 0, 0, 0);
                 }
             }
         }
     }
 
     // Normalise by the row sum (both lane halves hold partial sums) and store:
-    // lane holds context column j*32 + l32 of query rows 8*(r/4) + 4*half + r%4.
+    // lane holds dims j*32 + 8*g + 4*half + 0..3 (g = r / 4) of query l32.
     const float l_tot = l_run + __shfl_xor(l_run, 32);
+    const int q = q0 + l32;
+    if (q < len) {
+        const float inv = 1.0f / l_tot;
+        const int64_t at = (int64_t)(start + q) * H + head * HD + 4 * half;
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-        const int qrow = 8 * (r >> 2) + 4 * half + (r & 3);
-        const float lq = __shfl(l_tot, qrow);
-        const int q = q0 + qrow;
-        if (q < len) {
-            const int64_t at = (int64_t)(start + q) * H + head * HD + l32;
+        for (int j = 0; j < NJ; ++j)
 #pragma unroll
-            for (int j = 0; j < NJ; ++j) {
-                const float c = o[j][r] / lq;
-                if constexpr (OUT16) static_cast<uint16_t*>(ctx_out)[at + j * 32] = f32_to_bf16_rne(c);
-                else static_cast<float*>(ctx_out)[at + j * 32] = c;
+            for (int g = 0; g < 4; ++g) {
+                const float c0 = o[j][4 * g] * inv, c1 = o[j][4 * g + 1] * inv;
+                const float c2 = o[j][4 * g + 2] * inv, c3 = o[j][4 * g + 3] * inv;
+                const int64_t d = at + j * 32 + 8 * g;
+                if constexpr (OUT16) {
+                    uint2 h;
+                    h.x = (uint32_t)f32_to_bf16_rne(c0) | ((uint32_t)f32_to_bf16_rne(c1) << 16);
+                    h.y = (uint32_t)f32_to_bf16_rne(c2) | ((uint32_t)f32_to_bf16_rne(c3) << 16);
+                    *reinterpret_cast<uint2*>(static_cast<uint16_t*>(ctx_out) + d) = h;
+                } else {
+                    *reinterpret_cast<float4*>(static_cast<float*>(ctx_out) + d) = make_float4(c0, c1, c2, c3);
+                }
             }
-        }
     }
 }
 
@@ -307,13 +315,12 @@ __global__ __launch_bounds__(256) void attention_bf16_kernel(const uint16_t* __r
         m_run = m_new;
         if (c > 0) {
 #pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const float ar = __shfl(alpha, 8 * (r >> 2) + 4 * half + (r & 3));
+            for (int j = 0; j < NJ; ++j)
 #pragma unroll
-                for (int j = 0; j < NJ; ++j) o[j][r] *= ar;
-            }
+                for (int r = 0; r < 16; ++r) o[j][r] *= alpha;
         }
-        // context += P . V over this chunk, two 16-key MFMAs per 32-key block
+        // context^T += V^T . P^T over this chunk, two 16-key MFMAs per 32-key
+        // block: A = V^T (row = dim l32, this lane half's 8 keys), B = P^T.
 #pragma unroll
         for (int kb = 0; kb < 4; ++kb) {
             if (kb < nkb) {
@@ -333,8 +340,8 @@ __global__ __launch_bounds__(256) void attention_bf16_kernel(const uint16_t* __r
                         vb[2] = (short)(lo.y & 0xFFFF); vb[3] = (short)(lo.y >> 16);
                         vb[4] = (short)(hi.x & 0xFFFF); vb[5] = (short)(hi.x >> 16);
                         vb[6] = (short)(hi.y & 0xFFFF); vb[7] = (short)(hi.y >> 16);
-                        o[j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(v8bf_t, pa),
-                                                                        __builtin_bit_cast(v8bf_t, vb),
+                        o[j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(v8bf_t, vb),
+                                                                        __builtin_bit_cast(v8bf_t, pa),
                                                                         o[j], 0, 0, 0);
                     }
                 }
@@ -342,17 +349,21 @@ __global__ __launch_bounds__(256) void attention_bf16_kernel(const uint16_t* __r
         }
     }
 
+    // Lane holds dims j*32 + 8*g + 4*half + 0..3 (g = r / 4) of query l32.
     const float l_tot = l_run + __shfl_xor(l_run, 32);
+    const int q = q0 + l32;
+    if (q < len) {
+        const float inv = 1.0f / l_tot;
+        uint16_t* dst = ctx + (int64_t)(start + q) * H + head * HD + 4 * half;
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-        const int qrow = 8 * (r >> 2) + 4 * half + (r & 3);
-        const float lq = __shfl(l_tot, qrow);
-        const int q = q0 + qrow;
-        if (q < len) {
-            uint16_t* dst = ctx + (int64_t)(start + q) * H + head * HD + l32;
+        for (int j = 0; j < NJ; ++j)
 #pragma unroll
-            for (int j = 0; j < NJ; ++j) dst[j * 32] = f32_to_bf16_rne(o[j][r] / lq);
-        }
+            for (int g = 0; g < 4; ++g) {
+                uint2 h;
+                h.x = (uint32_t)f32_to_bf16_rne(o[j][4 * g] * inv) | ((uint32_t)f32_to_bf16_rne(o[j][4 * g + 1] * inv) << 16);
+                h.y = (uint32_t)f32_to_bf16_rne(o[j][4 * g + 2] * inv) | ((uint32_t)f32_to_bf16_rne(o[j][4 * g + 3] * inv) << 16);
+                *reinterpret_cast<uint2*>(dst + j * 32 + 8 * g) = h;
+            }
     }
 }
 

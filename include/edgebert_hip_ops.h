@@ -49,13 +49,14 @@ EBH_API int ebh_op_gemm_bf16(const uint16_t* A, int64_t lda, const uint16_t* W, 
 /* Masked multi-head attention (src/lib.rs:700-730 with 851-956) over packed
  * sequences: qkv [T, 3*hidden] rows (q | k | v), sequence b = rows
  * cu_seqlens[b] .. cu_seqlens[b+1]-1 (every row a real token, lengths <=
- * max_len); ctx [T, hidden].  head_dim = hidden / num_heads must be 32 or 64;
+ * max_len); ctx [T, hidden]; qkv and ctx 16-byte aligned.  head_dim = hidden /
+ * num_heads must be 32 or 64;
  * scale is 1/sqrt(head_dim) as the reference computes it (src/lib.rs:196-197). */
 EBH_API int ebh_op_attention(const float* qkv, const int32_t* cu_seqlens, int32_t B, int32_t max_len,
                      int32_t hidden, int32_t num_heads, float* ctx, void* stream);
 
 /* The same attention for bf16 models: qkv [T, 3*hidden] and ctx [T, hidden]
- * hold bf16 bit patterns (qkv 16-byte aligned); q.k^T, softmax and the P.V
+ * hold bf16 bit patterns (qkv 16-byte, ctx 8-byte aligned); q.k^T, softmax and the P.V
  * sums accumulate in fp32 (bf16 counterpart of the reference's fp32
  * attention, src/lib.rs:700-730). */
 EBH_API int ebh_op_attention_bf16(const uint16_t* qkv, const int32_t* cu_seqlens, int32_t B,
