@@ -68,6 +68,7 @@ struct Workspace {
     void* base = nullptr;
     int64_t tok_cap = 0;  // B*S tokens
     int b_cap = 0;
+    int y_parts = 1;      // Y holds y_parts * tok_cap rows (split-K partial products)
     float *X, *Y, *QKV, *CTX, *F;
     uint16_t* X16;  // bf16 copy of X (bf16 models: the GEMM input)
     int *ids, *mask, *counts, *cu, *ntok, *tok_id, *tok_pos, *err;
@@ -202,10 +203,16 @@ int ensure_workspace(ebh_model* m, int B, int S) {
     const int bcap = std::max(B, w.b_cap);
     const ebh_config& c = m->cfg;
     const size_t H = c.hidden_size, I = c.intermediate_size;
+    // Few-token fp32 forwards split the bias-free projections over K; Y then
+    // holds one partial product per split.
+    const int yparts = m->dtype == EBH_DTYPE_BF16
+                           ? 1
+                           : std::max(ebh::gemm_f32_splits((int)tcap, (int)H, (int)H),
+                                      ebh::gemm_f32_splits((int)tcap, (int)H, (int)I));
     size_t off = 0;
     auto take = [&](size_t bytes) { size_t o = off; off += align_up(std::max<size_t>(bytes, 1)); return o; };
     const size_t oX = take(tcap * H * 4), oX16 = take(m->dtype == EBH_DTYPE_BF16 ? tcap * H * 2 : 0),
-                 oY = take(tcap * H * 4), oQKV = take(tcap * 3 * H * 4),
+                 oY = take((size_t)yparts * tcap * H * 4), oQKV = take(tcap * 3 * H * 4),
                  oCTX = take(tcap * H * 4), oF = take(tcap * I * 4), oIds = take(tcap * 4),
                  oMask = take(tcap * 4), oCounts = take(bcap * 4), oCu = take((bcap + 1) * 4),
                  oNtok = take(4), oTid = take(tcap * 4), oTpos = take(tcap * 4), oErr = take(4),
@@ -222,6 +229,7 @@ int ensure_workspace(ebh_model* m, int B, int S) {
     w.base = base;
     w.tok_cap = tcap;
     w.b_cap = bcap;
+    w.y_parts = yparts;
     w.X = (float*)(b + oX);
     w.X16 = m->dtype == EBH_DTYPE_BF16 ? (uint16_t*)(b + oX16) : nullptr;
     w.Y = (float*)(b + oY);
@@ -292,8 +300,10 @@ int enqueue_forward(ebh_model* m, const int* d_ids, const int* d_mask, int B, in
     uint16_t* ctx16 = reinterpret_cast<uint16_t*>(w.CTX);
     uint16_t* f16 = reinterpret_cast<uint16_t*>(w.F);
     auto gemm = [&](int kind, const void* A, int64_t lda, const float* W32, const uint16_t* W16,
-                    const float* bias, void* C, int N, int K, int epi, bool c16) -> int {
+                    const float* bias, void* C, int N, int K, int epi, bool c16, int splits = 1) -> int {
         ebh::GemmArgs a{};
+        a.splits = splits;
+        a.split_stride = (int64_t)T * N;
         a.A = A;
         a.W = bf16 ? (const void*)W16 : (const void*)W32;
         a.bias = bias;
@@ -320,11 +330,23 @@ int enqueue_forward(ebh_model* m, const int* d_ids, const int* d_mask, int B, in
     // FFN-down projections are written without bias (as bf16 in bf16 models);
     // their bias and the block's residual are added in fp32, in the reference's
     // order, by the LayerNorm that follows.
-    auto add_ln = [&](const float* bias, const float* g, const float* b) -> hipError_t {
+    // With few tokens (fp32) these two products are split over K into partial
+    // outputs that the LayerNorm sums in a fixed order, so the result does not
+    // depend on timing.
+    auto add_ln = [&](const float* bias, const float* g, const float* b, int parts) -> hipError_t {
         return bf16 ? ebh::launch_add_layernorm_y16(reinterpret_cast<const uint16_t*>(w.Y), bias, w.X, g, b, T,
                                                     w.ntok, H, eps, w.X16, s)
-                    : ebh::launch_add_layernorm(w.Y, bias, w.X, g, b, T, w.ntok, H, eps, w.X16, s);
+                    : ebh::launch_add_layernorm(w.Y, bias, w.X, g, b, T, w.ntok, H, eps, w.X16, s, parts,
+                                                (int64_t)T * H);
     };
+    const int64_t part_cap = (int64_t)w.y_parts * w.tok_cap / std::max<int64_t>(T, 1);
+    auto splits_for = [&](int K) {
+        if (bf16) return 1;
+        int sp = ebh::gemm_f32_splits(T, H, K);
+        while (sp > 1 && sp > part_cap) sp /= 2;
+        return sp;
+    };
+    const int sp_out = splits_for(H), sp_down = splits_for(I);
     for (const DevLayer& L : m->layers) {
         int rc;
         if ((rc = gemm(EBH_PROF_GEMM_QKV, bf16 ? (const void*)w.X16 : w.X, H, L.wqkv, L.wqkv16, L.bqkv,
@@ -337,19 +359,19 @@ int enqueue_forward(ebh_model* m, const int* d_ids, const int* d_mask, int B, in
             HIP_TRY(ebh::launch_attention(w.QKV, w.cu, B, S, H, nh, hd, scale, w.CTX, false, s));
         prof_end(m, s, pp, on);
         if ((rc = gemm(EBH_PROF_GEMM_OUT, bf16 ? (const void*)ctx16 : w.CTX, H, L.wo, L.wo16, nullptr,
-                       w.Y, H, H, ebh::EPI_NONE, bf16)))
+                       w.Y, H, H, ebh::EPI_NONE, bf16, sp_out)))
             return rc;
         prof_begin(m, EBH_PROF_LAYERNORM, s, pp, on);
-        HIP_TRY(add_ln(L.bo, L.ln1_g, L.ln1_b));
+        HIP_TRY(add_ln(L.bo, L.ln1_g, L.ln1_b, sp_out));
         prof_end(m, s, pp, on);
         if ((rc = gemm(EBH_PROF_GEMM_FFN_UP, bf16 ? (const void*)w.X16 : w.X, H, L.w1, L.w116, L.b1,
                        bf16 ? (void*)f16 : (void*)w.F, I, H, ebh::EPI_BIAS_GELU, bf16)))
             return rc;
         if ((rc = gemm(EBH_PROF_GEMM_FFN_DOWN, bf16 ? (const void*)f16 : w.F, I, L.w2, L.w216, nullptr,
-                       w.Y, H, I, ebh::EPI_NONE, bf16)))
+                       w.Y, H, I, ebh::EPI_NONE, bf16, sp_down)))
             return rc;
         prof_begin(m, EBH_PROF_LAYERNORM, s, pp, on);
-        HIP_TRY(add_ln(L.b2, L.ln2_g, L.ln2_b));
+        HIP_TRY(add_ln(L.b2, L.ln2_g, L.ln2_b, sp_down));
         prof_end(m, s, pp, on);
     }
     prof_begin(m, EBH_PROF_POOL, s, pp, on);

@@ -464,12 +464,16 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_persistent_kernel
     const int N = p.N;
     const int ntiles_n = (N + BN - 1) / BN;
     const int ntiles = ((M + BM - 1) / BM) * ntiles_n;
-    const int nk = p.K / BK;
+    // Split-K: work item u covers C tile u % ntiles over k-range u / ntiles
+    // (split-major, so an XCD's consecutive items still share A row panels).
+    const int S = p.splits > 1 ? p.splits : 1;
+    const int nwork = ntiles * S;
+    const int nk = p.K / BK / S;                  // k-tiles per work item
     // Workgroup b runs on XCD b % 8: renumber so each XCD's workgroups take
     // consecutive tiles (N-fastest), which share A row panels in that XCD's L2.
     const int G = gridDim.x;
     const int wg = (G & 7) == 0 ? (blockIdx.x & 7) * (G >> 3) + (blockIdx.x >> 3) : blockIdx.x;
-    const int my_tiles = wg < ntiles ? (ntiles - wg + G - 1) / G : 0;
+    const int my_tiles = wg < nwork ? (nwork - wg + G - 1) / G : 0;
     const int total = my_tiles * nk;
     if (total == 0) return;  // uniform over the workgroup
 
@@ -493,7 +497,8 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_persistent_kernel
     const float* bias_src = nullptr;
     int nit = 0;
     auto point_at = [&](int it) {
-        const int t = wg + (it / nk) * G, kt = it - (it / nk) * nk;
+        const int u = wg + (it / nk) * G, split = u / ntiles, t = u - split * ntiles;
+        const int kt = split * nk + it - (it / nk) * nk;
         const int mt = t / ntiles_n, m0 = mt * BM, n0 = (t - mt * ntiles_n) * BN;
 #pragma unroll
         for (int i = 0; i < NL; ++i)
@@ -530,7 +535,8 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_persistent_kernel
     v16f acc[FM][FN];
     // Epilogue of local tile t: bias (+ GELU), C through LDS stage `cs`, float4 stores.
     auto epilogue_tile = [&](int t, const float* cs_base) {
-        const int tile = wg + t * G;
+        const int u = wg + t * G, split = u / ntiles, tile = u - split * ntiles;
+        float* const Cs = p.C + (int64_t)split * p.split_stride;
         const int m0 = (tile / ntiles_n) * BM, n0 = (tile - (tile / ntiles_n) * ntiles_n) * BN;
         const int gc = n0 + wn * WN + e_c;
         const bool col_ok = gc < N;  // N % 4 == 0: all 4 columns or none
@@ -560,9 +566,9 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_persistent_kernel
                         uint2 h;
                         h.x = (uint32_t)f32_to_bf16_rne(v.x) | ((uint32_t)f32_to_bf16_rne(v.y) << 16);
                         h.y = (uint32_t)f32_to_bf16_rne(v.z) | ((uint32_t)f32_to_bf16_rne(v.w) << 16);
-                        *reinterpret_cast<uint2*>(reinterpret_cast<uint16_t*>(p.C) + (int64_t)row * p.ldc + gc) = h;
+                        *reinterpret_cast<uint2*>(reinterpret_cast<uint16_t*>(Cs) + (int64_t)row * p.ldc + gc) = h;
                     } else {
-                        *reinterpret_cast<float4*>(p.C + (int64_t)row * p.ldc + gc) = v;
+                        *reinterpret_cast<float4*>(Cs + (int64_t)row * p.ldc + gc) = v;
                     }
                 }
             }
@@ -874,22 +880,34 @@ hipError_t launch_gemm_f32(const GemmArgs& a, int epi, hipStream_t s) {
     //    tokens): 32-deep k-tiles, two workgroups per CU, so one workgroup's
     //    GELU epilogue runs beside the other's MFMAs;
     //  * otherwise 128 x 128 tiles, 64-deep k-tiles, 8 waves (two per SIMD).
+    //  * split-K (a.splits > 1, bias-free products only): each split is a work
+    //    item of its own, written to its own partial output.
+    const int S = a.splits > 1 ? a.splits : 1;
+    if (S > 1 && (epi != EPI_NONE || !ok || a.K % (32 * S))) return hipErrorInvalidValue;
     const int64_t tiles128 = (int64_t)((a.M_max + 127) / 128) * ((a.N + 127) / 128);
-    if (ok && a.K % 64 == 0 && 2 * tiles128 < (int64_t)cu_count())
+    if (ok && a.K % (64 * S) == 0 && 2 * tiles128 < (int64_t)cu_count())
         return launch_persistent<64, 64, 64, 2, 2, 2>(a, epi, s, 2);
-    if (ok && a.K % 32 == 0 && a.N >= 1536 && a.K < 1024 && tiles128 >= 8 * (int64_t)cu_count())
+    if (ok && a.K % 32 == 0 && a.N >= 1536 && a.K < 1024 && tiles128 >= 8 * (int64_t)cu_count() && S == 1)
         return launch_persistent<128, 128, 32, 2, 2, 2>(a, epi, s, 2);
-    if (ok && a.K % 64 == 0)
+    if (ok && a.K % (64 * S) == 0)
         return launch_persistent<128, 128, 64, 2, 4, 2>(a, epi, s, 1);
-    if (ok && a.K % 32 == 0)
+    if (ok && a.K % (32 * S) == 0)
         return launch_persistent<128, 128, 32, 2, 2, 2>(a, epi, s, 2);
     return launch_tile<128, 128, 32, 2, 2, false>(a, epi, s);
+}
+
+int gemm_f32_splits(int M_max, int N, int K) {
+    const int64_t tiles128 = (int64_t)((M_max + 127) / 128) * ((N + 127) / 128);
+    if (2 * tiles128 >= (int64_t)cu_count()) return 1;   // enough tiles
+    for (int S : {4, 2})
+        if (K % (64 * S) == 0 && K / S >= 128) return S;
+    return 1;
 }
 
 // bf16 activations: 256 x 256 tiles, 64-deep k-tiles (8 chunks of 8), 8 waves
 // of 128 x 64, two LDS stages (2 x 64 KB), one workgroup per CU.
 hipError_t launch_gemm_bf16_act(const GemmArgs& a, int epi, bool c_bf16, hipStream_t s) {
-    const bool ok = epi != EPI_BIAS_RESID && aligned16(a.A) && aligned16(a.W) && aligned16(a.C) &&
+    const bool ok = epi != EPI_BIAS_RESID && a.splits <= 1 && aligned16(a.A) && aligned16(a.W) && aligned16(a.C) &&
                     (epi == EPI_NONE || aligned16(a.bias)) && a.lda % 8 == 0 && a.ldw % 8 == 0 &&
                     a.ldc % 4 == 0 && a.N % 4 == 0 && a.K % 64 == 0 && a.K > 0;
     if (!ok) return hipErrorInvalidValue;

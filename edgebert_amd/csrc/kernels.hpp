@@ -20,7 +20,16 @@ struct GemmArgs {
     int M_max;           // grid is sized for this many rows
     const int* M_dev;    // actual rows, read on device (nullptr: M_max)
     int N, K;
+    // Split-K (EPI_NONE only): split s of `splits` (0 or 1: no split) sums k in
+    // [s*K/splits, (s+1)*K/splits) into C + s * split_stride.
+    int splits;
+    int64_t split_stride;
 };
+
+// Split count launch_gemm_f32 takes best for a bias-free product of this shape
+// (1 unless there are too few tiles to fill the chip); the caller provides
+// `splits` partial outputs.
+int gemm_f32_splits(int M_max, int N, int K);
 
 // C = epi(A . W^T + bias); W fp32 (gemm_f32) or bf16 (gemm_bf16, A rounded to bf16).
 hipError_t launch_gemm_f32(const GemmArgs& a, int epi, hipStream_t s);
@@ -48,11 +57,14 @@ hipError_t launch_gemm_bf16_act(const GemmArgs& a, int epi, bool c_bf16, hipStre
 hipError_t launch_layernorm(const float* x, float* y, const float* g, const float* b,
                             int rows_max, const int* rows_dev, int H, float eps, hipStream_t s);
 
-// x = LayerNorm((y + bias) + x) per row, in place on x.
+// x = LayerNorm((y + bias) + x) per row, in place on x.  y may come as
+// nparts split-K partial products part_stride floats apart; they are summed in
+// order (((p0 + p1) + p2) + ...) before the bias.
 // x16 (optional): bf16 copy of the result (the input of bf16 GEMMs).
 hipError_t launch_add_layernorm(const float* y, const float* bias, float* x, const float* g,
                                 const float* b, int rows_max, const int* rows_dev, int H, float eps,
-                                uint16_t* x16, hipStream_t s);
+                                uint16_t* x16, hipStream_t s, int nparts = 1,
+                                int64_t part_stride = 0);
 // The same with y stored as bf16 (bf16 models).  Needs 8-byte aligned bf16
 // rows, 16-byte aligned fp32 operands and row4_shape_ok(H).
 // H = 4 * L * n with L lanes per row in {64, 32, 16} and n float4 per lane in

@@ -165,7 +165,8 @@ __global__ __launch_bounds__(256) void add_layernorm_kernel(const float* __restr
                                                             float* x, const float* __restrict__ g,
                                                             const float* __restrict__ bta,
                                                             int rows_max, const int* rows_dev,
-                                                            int H, float eps, uint16_t* x16) {
+                                                            int H, float eps, uint16_t* x16,
+                                                            int nparts, int64_t part_stride) {
     const int row = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
     const int rows = rows_dev ? *rows_dev : rows_max;
     if (row >= rows) return;
@@ -175,7 +176,12 @@ __global__ __launch_bounds__(256) void add_layernorm_kernel(const float* __restr
 #pragma unroll
     for (int c = 0; c < NC; ++c) {
         const int i = c * 64 + lane;
-        v[c] = i < H ? (yr[i] + bias[i]) + xr[i] : 0.0f;
+        float yv = 0.0f;
+        if (i < H) {
+            yv = yr[i];
+            for (int q = 1; q < nparts; ++q) yv += yr[q * part_stride + i];
+        }
+        v[c] = i < H ? (yv + bias[i]) + xr[i] : 0.0f;
     }
     ln_row<NC>(v, lane, H, g, bta, eps, xr, x16 ? x16 + (int64_t)row * H : nullptr);
 }
@@ -263,7 +269,8 @@ __global__ __launch_bounds__(256) void add_layernorm4_kernel(const float* __rest
                                                              float* x, const float* __restrict__ g,
                                                              const float* __restrict__ bta,
                                                              int rows_max, const int* rows_dev,
-                                                             int H, float eps, uint16_t* x16) {
+                                                             int H, float eps, uint16_t* x16,
+                                                             int nparts, int64_t part_stride) {
     constexpr int RPB = 256 / LPR;                // rows per workgroup
     const int row = blockIdx.x * RPB + threadIdx.x / LPR, sub = threadIdx.x % LPR;
     const int rows = rows_dev ? *rows_dev : rows_max;
@@ -274,7 +281,11 @@ __global__ __launch_bounds__(256) void add_layernorm4_kernel(const float* __rest
 #pragma unroll
     for (int c = 0; c < NV; ++c) {
         const int i = 4 * (c * LPR + sub);
-        const float4 a = *reinterpret_cast<const float4*>(yr + i);
+        float4 a = *reinterpret_cast<const float4*>(yr + i);
+        for (int q = 1; q < nparts; ++q) {        // split-K partials, in order
+            const float4 pq = *reinterpret_cast<const float4*>(yr + q * part_stride + i);
+            a.x += pq.x; a.y += pq.y; a.z += pq.z; a.w += pq.w;
+        }
         const float4 bb = *reinterpret_cast<const float4*>(bias + i);
         const float4 r = *reinterpret_cast<const float4*>(xr + i);
         v[c] = make_float4((a.x + bb.x) + r.x, (a.y + bb.y) + r.y, (a.z + bb.z) + r.z, (a.w + bb.w) + r.w);
@@ -405,17 +416,20 @@ hipError_t launch_layernorm(const float* x, float* y, const float* g, const floa
 
 hipError_t launch_add_layernorm(const float* y, const float* bias, float* x, const float* g,
                                 const float* b, int rows_max, const int* rows_dev, int H, float eps,
-                                uint16_t* x16, hipStream_t s) {
+                                uint16_t* x16, hipStream_t s, int nparts, int64_t part_stride) {
     if (rows_max <= 0) return hipSuccess;
+    if (nparts < 1) nparts = 1;
     int lpr, nv;
     row4_shape(H, lpr, nv);
-    if (lpr && al16(y) && al16(bias) && al16(x) && al16(g) && al16(b) && (!x16 || ((uintptr_t)x16 & 7) == 0)) {
+    if (lpr && al16(y) && al16(bias) && al16(x) && al16(g) && al16(b) && (!x16 || ((uintptr_t)x16 & 7) == 0) &&
+        part_stride % 4 == 0) {
         EBH_ROW4_DISPATCH(add_layernorm4_kernel, lpr, nv, rows_max, s, y, bias, x, g, b, rows_max,
-                          rows_dev, H, eps, x16);
+                          rows_dev, H, eps, x16, nparts, part_stride);
         return hipGetLastError();
     }
     const dim3 grid((rows_max + 3) / 4);
-    EBH_ROW_DISPATCH(add_layernorm_kernel, H, grid, s, y, bias, x, g, b, rows_max, rows_dev, H, eps, x16);
+    EBH_ROW_DISPATCH(add_layernorm_kernel, H, grid, s, y, bias, x, g, b, rows_max, rows_dev, H, eps, x16,
+                     nparts, part_stride);
     return hipGetLastError();
 }
 
