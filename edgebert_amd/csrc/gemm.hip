@@ -433,7 +433,8 @@ __device__ __forceinline__ float gelu_tanh_fast(float val) {
 // (chunk = 4 elements, four v_mfma_f32_32x32x2_f32).  OUT16: C is written as
 // bf16 (round to nearest even) instead of fp32.  LDS offsets below are in
 // 4-byte words, so both element types share the layout and the swizzle.
-template <bool BF16, bool OUT16, int BM, int BN, int BK, int WAVES_M, int WAVES_N, int NSTAGE, int EPI>
+template <bool BF16, bool OUT16, int BM, int BN, int BK, int WAVES_M, int WAVES_N, int NSTAGE, int EPI,
+          bool SPREAD = BF16>
 __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_persistent_kernel(GemmArgs p) {
     constexpr int ES = BF16 ? 2 : 4;              // bytes per element
     constexpr int EPC = 16 / ES;                  // elements per 16-byte chunk
@@ -508,22 +509,38 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_persistent_kernel
     };
     // Load instructions of k-tile j (the bias chunk rides with a tile's first k-tile).
     auto n_issued = [&](int j) { return NL + (HAS_BIAS && j % nk == 0 ? 1 : 0); };
-    auto issue = [&]() {
+    // The loads of a k-tile go out in parts: all at once, or (SPREAD) one part
+    // before each k-slice's MFMAs.  The CU's vector memory path takes about
+    // one 1 KB load per 20 cycles and a wave stalls at issue while it is backed
+    // up; at bf16 rates a k-tile's loads need over half of its MFMA time on
+    // that path, so issuing them as one burst after the barrier would idle the
+    // MFMA pipes.  Part `part` of NPART issues loads [part * PER, (part + 1) *
+    // PER); the last part adds the bias chunk and moves on to the next k-tile.
+    constexpr int NPART = SPREAD ? KS : 1;
+    constexpr int PER = (NL + NPART - 1) / NPART;
+    auto issue_part = [&](int part) {
         float* st = smem + (nit % NSTAGE) * STAGE;
 #pragma unroll
         for (int i = 0; i < NL; ++i)
-            load_lds16_async(src[i], st + (i < LA ? 0 : BM * RW) + ((i < LA ? i : i - LA) * NT + wave * 64) * 4);
-        if (HAS_BIAS && nit % nk == 0)
-            load_lds16_async(bias_src, smem + NSTAGE * STAGE + (((nit / nk) & 1) * NW + wave) * BIAS_SLOT);
-        ++nit;
-        if (nit < total) {
-            if (nit % nk == 0) {
-                point_at(nit);
-            } else {
+            if (i / PER == part)
+                load_lds16_async(src[i], st + (i < LA ? 0 : BM * RW) + ((i < LA ? i : i - LA) * NT + wave * 64) * 4);
+        if (part == NPART - 1) {
+            if (HAS_BIAS && nit % nk == 0)
+                load_lds16_async(bias_src, smem + NSTAGE * STAGE + (((nit / nk) & 1) * NW + wave) * BIAS_SLOT);
+            ++nit;
+            if (nit < total) {
+                if (nit % nk == 0) {
+                    point_at(nit);
+                } else {
 #pragma unroll
-                for (int i = 0; i < NL; ++i) src[i] += BK * ES;
+                    for (int i = 0; i < NL; ++i) src[i] += BK * ES;
+                }
             }
         }
+    };
+    auto issue = [&]() {
+#pragma unroll
+        for (int part = 0; part < NPART; ++part) issue_part(part);
     };
 
     const int sw = chunk_swizzle16<CPR>(l32);
@@ -599,10 +616,12 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_persistent_kernel
 #pragma unroll
                         for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
             }
-            if (nit < total) issue();
+            const bool refill = nit < total;
+            if (!SPREAD && refill) issue();
             const float* st = smem + (it % NSTAGE) * STAGE;
 #pragma unroll
             for (int s = 0; s < KS; ++s) {
+                if (SPREAD && refill) issue_part(s);
                 const int ko = 4 * ((2 * s + half) ^ sw);
                 v4f af[FM], wf[FN];
 #pragma unroll
