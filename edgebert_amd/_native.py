@@ -56,6 +56,8 @@ _SIGS = {
     "ebh_forward": (_i32, [_vp, _vp, _vp, _i32, _i32, _vp]),
     "ebh_encode": (_i32, [_vp, _vp, _vp, _i32, _i32, _i32, _vp]),
     "ebh_encode_device": (_i32, [_vp, _vp, _vp, _i32, _i32, _i32, _vp, _vp]),
+    "ebh_score": (_i32, [_vp, _vp, _vp, _i32, _i32, _vp]),
+    "ebh_score_device": (_i32, [_vp, _vp, _vp, _i32, _i32, _vp, _vp]),
     "ebh_synchronize": (_i32, [_vp]),
     "ebh_last_tokens": (_i32, [_vp, _vp, _vp, _i64, _vp, _i64, _vp]),
     "ebh_model_info": (_i32, [_vp, ctypes.POINTER(EbhConfig), ctypes.POINTER(_i32)]),

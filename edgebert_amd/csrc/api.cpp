@@ -73,6 +73,7 @@ struct Workspace {
     uint16_t* X16;  // bf16 copy of X (bf16 models: the GEMM input)
     int *ids, *mask, *counts, *cu, *ntok, *tok_id, *tok_pos, *err;
     float* out;
+    float* scores;  // [B] cross-encoder scores
 };
 
 struct ProfPair {
@@ -91,6 +92,9 @@ struct ebh_model {
     void* wbase = nullptr;
     float *word, *pos, *type0, *emb_g, *emb_b;
     std::vector<DevLayer> layers;
+    // cross-encoder head (classifier.weight [H], classifier.bias), when loaded
+    bool cross_encoder = false;
+    float *cls_w = nullptr, *cls_b = nullptr;
     hipStream_t stream = nullptr;
     hipEvent_t done = nullptr;  // completion of the last enqueued forward
     bool has_done = false;
@@ -216,7 +220,7 @@ int ensure_workspace(ebh_model* m, int B, int S) {
                  oCTX = take(tcap * H * 4), oF = take(tcap * I * 4), oIds = take(tcap * 4),
                  oMask = take(tcap * 4), oCounts = take(bcap * 4), oCu = take((bcap + 1) * 4),
                  oNtok = take(4), oTid = take(tcap * 4), oTpos = take(tcap * 4), oErr = take(4),
-                 oOut = take((size_t)bcap * H * 4);
+                 oOut = take((size_t)bcap * H * 4), oScores = take((size_t)bcap * 4);
     // Work from the previous call may still use the old block.
     if (m->has_done) HIP_TRY(hipEventSynchronize(m->done));
     if (w.base) HIP_TRY(hipFree(w.base));
@@ -245,6 +249,7 @@ int ensure_workspace(ebh_model* m, int B, int S) {
     w.tok_pos = (int*)(b + oTpos);
     w.err = (int*)(b + oErr);
     w.out = (float*)(b + oOut);
+    w.scores = (float*)(b + oScores);
     HIP_TRY(hipMemset(w.err, 0, 4));
     return EBH_OK;
 }
@@ -271,8 +276,10 @@ int ensure_host_staging(ebh_model* m, int64_t T, int64_t outn) {
 }
 
 // Enqueue the whole forward on stream s (ids/mask already in device memory).
+// d_scores (optional, cross-encoders): score[b] = pooled[b] . w + bias, from
+// the un-normalised pooled rows left in d_out.
 int enqueue_forward(ebh_model* m, const int* d_ids, const int* d_mask, int B, int S,
-                    int normalize, float* d_out, hipStream_t s) {
+                    int normalize, float* d_out, hipStream_t s, float* d_scores = nullptr) {
     const ebh_config& c = m->cfg;
     const int H = c.hidden_size, I = c.intermediate_size, nh = c.num_attention_heads;
     const int hd = H / nh;
@@ -377,6 +384,7 @@ int enqueue_forward(ebh_model* m, const int* d_ids, const int* d_mask, int B, in
     prof_begin(m, EBH_PROF_POOL, s, pp, on);
     HIP_TRY(ebh::launch_pool(w.X, w.cu, B, H, S, normalize, d_out, s));
     prof_end(m, s, pp, on);
+    if (d_scores) HIP_TRY(ebh::launch_cls_head(d_out, m->cls_w, m->cls_b, B, H, d_scores, s));
     HIP_TRY(hipEventRecord(m->done, s));
     m->has_done = true;
     m->last_B = B;
@@ -384,21 +392,26 @@ int enqueue_forward(ebh_model* m, const int* d_ids, const int* d_mask, int B, in
 }
 
 // Blocking forward from int32 host ids/mask already validated into h_ids/h_mask.
-int forward_host_staged(ebh_model* m, int B, int S, int normalize, float* out) {
+// Staged host ids / mask -> device forward -> out ([B, H], or the [B]
+// cross-encoder scores when `score`).
+int forward_host_staged(ebh_model* m, int B, int S, int normalize, float* out, bool score = false) {
     const int64_t T = (int64_t)B * S;
     const int H = m->cfg.hidden_size;
+    const size_t n_out = score ? (size_t)B : (size_t)B * H;
     hipStream_t s = m->stream;
     int rc = ensure_workspace(m, B, S);
     if (rc) return rc;
     if (m->has_done) HIP_TRY(hipStreamWaitEvent(s, m->done, 0));
     HIP_TRY(hipMemcpyAsync(m->ws.ids, m->h_ids, T * 4, hipMemcpyHostToDevice, s));
     HIP_TRY(hipMemcpyAsync(m->ws.mask, m->h_mask, T * 4, hipMemcpyHostToDevice, s));
-    if ((rc = enqueue_forward(m, m->ws.ids, m->ws.mask, B, S, normalize, m->ws.out, s))) return rc;
-    HIP_TRY(hipMemcpyAsync(m->h_out, m->ws.out, (size_t)B * H * 4, hipMemcpyDeviceToHost, s));
+    if ((rc = enqueue_forward(m, m->ws.ids, m->ws.mask, B, S, normalize, m->ws.out, s,
+                              score ? m->ws.scores : nullptr)))
+        return rc;
+    HIP_TRY(hipMemcpyAsync(m->h_out, score ? m->ws.scores : m->ws.out, n_out * 4, hipMemcpyDeviceToHost, s));
     HIP_TRY(hipMemcpyAsync(m->h_err, m->ws.err, 4, hipMemcpyDeviceToHost, s));
     HIP_TRY(hipStreamSynchronize(s));
     if (*m->h_err) return fail(EBH_ERR_RANGE, "token id out of range for vocab %d", m->cfg.vocab_size);
-    memcpy(out, m->h_out, (size_t)B * H * 4);
+    memcpy(out, m->h_out, n_out * 4);
     return EBH_OK;
 }
 
@@ -442,6 +455,28 @@ int ebh_set_tensor(ebh_model* m, const char* name, const float* data, const int6
                    int32_t ndim) {
     if (!m || !name || !shape || (!data && ndim > 0)) return fail(EBH_ERR_INVALID_ARG, "null argument");
     if (m->finalized) return fail(EBH_ERR_STATE, "model already finalized");
+    const std::string nm(name);
+    if (nm == "classifier.weight" || nm == "classifier.bias") {
+        // Cross-encoder head (from_cross_encoder_weights, src/lib.rs:385-399).
+        // The weight is taken as [H] (get_array1, src/weights.rs:47-58) or as
+        // the [1, H] a sequence-classification checkpoint stores; the bias must
+        // hold exactly one value (get_scalar, src/weights.rs:99-111).
+        int64_t n = 1;
+        for (int i = 0; i < ndim; ++i) n *= shape[i];
+        if (nm == "classifier.weight") {
+            const int64_t H = m->cfg.hidden_size;
+            const bool ok = (ndim == 1 && shape[0] == H) || (ndim == 2 && shape[0] == 1 && shape[1] == H);
+            if (!ok)
+                return fail(EBH_ERR_SHAPE, "Expected 1D tensor, got shape %s for %s (hidden size %lld)",
+                            shape_str(shape, ndim).c_str(), name, (long long)H);
+        } else if (n != 1) {
+            return fail(EBH_ERR_SHAPE, "Expected scalar, got %lld elements", (long long)n);
+        }
+        HostTensor& t = m->host[nm];
+        t.shape.assign(shape, shape + ndim);
+        t.data.assign(data, data + n);
+        return EBH_OK;
+    }
     std::vector<int64_t> storage;
     const std::vector<int64_t>* exp = expected_shape(m->cfg, name, storage);
     if (!exp) return fail(EBH_ERR_NOT_FOUND, "unknown tensor %s", name);
@@ -473,6 +508,9 @@ int ebh_finalize(ebh_model* m, int32_t dtype) {
     const auto names = expected_tensors(m->cfg);
     for (auto& kv : names)
         if (!m->host.count(kv.first)) return fail(EBH_ERR_NOT_FOUND, "Tensor %s not found", kv.first.c_str());
+    const bool has_cw = m->host.count("classifier.weight") > 0, has_cb = m->host.count("classifier.bias") > 0;
+    if (has_cw != has_cb)
+        return fail(EBH_ERR_NOT_FOUND, "Tensor %s not found", has_cw ? "classifier.bias" : "classifier.weight");
 
     const ebh_config& c = m->cfg;
     const size_t H = c.hidden_size, I = c.intermediate_size, L = c.num_hidden_layers;
@@ -492,6 +530,7 @@ int ebh_finalize(ebh_model* m, int32_t dtype) {
         o.w2 = take(H * I * 4); o.b2 = take(H * 4);
         o.ln2_g = take(H * 4); o.ln2_b = take(H * 4);
     }
+    const size_t oClsW = has_cw ? take(H * 4) : 0, oClsB = has_cw ? take(4) : 0;
     const size_t f32_bytes = off;
     if (dtype == EBH_DTYPE_BF16)
         for (size_t l = 0; l < L; ++l) {
@@ -533,6 +572,10 @@ int ebh_finalize(ebh_model* m, int32_t dtype) {
         put(o.ln2_g, p + "output.LayerNorm.weight");
         put(o.ln2_b, p + "output.LayerNorm.bias");
     }
+    if (has_cw) {
+        put(oClsW, "classifier.weight");
+        put(oClsB, "classifier.bias");
+    }
 
     HIP_TRY(hipGetDevice(&m->device));
     HIP_TRY(hipStreamCreateWithFlags(&m->stream, hipStreamNonBlocking));
@@ -545,6 +588,9 @@ int ebh_finalize(ebh_model* m, int32_t dtype) {
     m->type0 = (float*)(b + oType);
     m->emb_g = (float*)(b + oEg);
     m->emb_b = (float*)(b + oEb);
+    m->cross_encoder = has_cw;
+    m->cls_w = has_cw ? (float*)(b + oClsW) : nullptr;
+    m->cls_b = has_cw ? (float*)(b + oClsB) : nullptr;
     m->layers.resize(L);
     for (size_t l = 0; l < L; ++l) {
         const Off& o = lo[l];
@@ -670,6 +716,48 @@ int ebh_encode_device(ebh_model* m, const int32_t* ids, const int32_t* mask, int
     }
     if ((rc = ensure_workspace(m, B, S))) return rc;
     return enqueue_forward(m, ids, mask, B, S, normalize ? 1 : 0, out, s);
+}
+
+int ebh_score(ebh_model* m, const uint32_t* ids, const uint32_t* mask, int32_t B, int32_t S,
+              float* scores) {
+    int rc = check_model_ready(m);
+    if (rc) return rc;
+    if (!m->cross_encoder) return fail(EBH_ERR_STATE, "Model is not a cross-encoder");
+    if ((rc = check_dims(m, B, S))) return rc;
+    if (B == 0) return EBH_OK;
+    if (!ids || !mask || !scores) return fail(EBH_ERR_INVALID_ARG, "null buffer");
+    if (S == 0) return fail(EBH_ERR_INVALID_ARG, "empty pair encoding (S == 0)");
+    std::lock_guard<std::mutex> lk(m->mu);
+    HIP_TRY(hipSetDevice(m->device));
+    const int64_t T = (int64_t)B * S;
+    if ((rc = ensure_host_staging(m, T, (int64_t)B * m->cfg.hidden_size))) return rc;
+    for (int64_t i = 0; i < T; ++i) {
+        if (ids[i] >= (uint32_t)m->cfg.vocab_size)
+            return fail(EBH_ERR_RANGE, "token id %u at [%lld, %lld] out of range for vocab %d",
+                        ids[i], (long long)(i / S), (long long)(i % S), m->cfg.vocab_size);
+        if (mask[i] > 1)
+            return fail(EBH_ERR_INVALID_ARG, "attention mask value %u at [%lld, %lld] is not 0 or 1",
+                        mask[i], (long long)(i / S), (long long)(i % S));
+        m->h_ids[i] = (int)ids[i];
+        m->h_mask[i] = (int)mask[i];
+    }
+    return forward_host_staged(m, B, S, 0, scores, true);
+}
+
+int ebh_score_device(ebh_model* m, const int32_t* ids, const int32_t* mask, int32_t B, int32_t S,
+                     float* scores, void* stream) {
+    int rc = check_model_ready(m);
+    if (rc) return rc;
+    if (!m->cross_encoder) return fail(EBH_ERR_STATE, "Model is not a cross-encoder");
+    if ((rc = check_dims(m, B, S))) return rc;
+    if (B == 0) return EBH_OK;
+    if (!ids || !mask || !scores) return fail(EBH_ERR_INVALID_ARG, "null buffer");
+    if (S == 0) return fail(EBH_ERR_INVALID_ARG, "empty pair encoding (S == 0)");
+    std::lock_guard<std::mutex> lk(m->mu);
+    HIP_TRY(hipSetDevice(m->device));
+    hipStream_t s = stream ? static_cast<hipStream_t>(stream) : m->stream;
+    if ((rc = ensure_workspace(m, B, S))) return rc;
+    return enqueue_forward(m, ids, mask, B, S, 0, m->ws.out, s, scores);
 }
 
 int ebh_synchronize(ebh_model* m) {

@@ -88,6 +88,10 @@ hipError_t launch_embed_ln(const int* tok_id, const int* tok_pos, const int* n_t
 hipError_t launch_pool(const float* x, const int* cu_seqlens, int B, int H, int S,
                        int normalize, float* out, hipStream_t s);
 
+// Cross-encoder head: out[b] = pooled[b] . w + bias[0] (pooled [B, H], w [H]).
+hipError_t launch_cls_head(const float* pooled, const float* w, const float* bias, int B, int H,
+                           float* out, hipStream_t s);
+
 // fp32 -> bf16 (round to nearest even) for weight upload.
 hipError_t launch_f32_to_bf16(const float* x, uint16_t* y, int64_t n, hipStream_t s);
 

@@ -559,6 +559,29 @@ hipError_t launch_pool(const float* x, const int* cu_seqlens, int B, int H, int 
     return hipGetLastError();
 }
 
+// Cross-encoder head (Model::score_pair, src/lib.rs:363-375): score[b] =
+// pooled[b] . w + bias, one wave per row (the products summed in lane order,
+// then a butterfly over the wave).
+__global__ __launch_bounds__(256) void cls_head_kernel(const float* __restrict__ pooled,
+                                                       const float* __restrict__ w,
+                                                       const float* __restrict__ bias, int B, int H,
+                                                       float* __restrict__ out) {
+    const int b = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+    if (b >= B) return;
+    const float* x = pooled + (int64_t)b * H;
+    float acc = 0.0f;
+    for (int i = lane; i < H; i += 64) acc += x[i] * w[i];
+    acc = wave_sum(acc);
+    if (lane == 0) out[b] = acc + bias[0];
+}
+
+hipError_t launch_cls_head(const float* pooled, const float* w, const float* bias, int B, int H,
+                           float* out, hipStream_t s) {
+    if (B <= 0) return hipSuccess;
+    hipLaunchKernelGGL(cls_head_kernel, dim3((B + 3) / 4), dim3(256), 0, s, pooled, w, bias, B, H, out);
+    return hipGetLastError();
+}
+
 // ---------------------------------------------------------------------------
 __global__ void f32_to_bf16_kernel(const float* __restrict__ x, uint16_t* __restrict__ y,
                                    int64_t n) {

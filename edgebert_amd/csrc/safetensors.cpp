@@ -202,8 +202,9 @@ extern "C" int ebh_load_safetensors(ebh_model* m, const char* path) {
         const JVal& t = kv.second;
         if (t.kind != JVal::OBJ || !t.obj.count("dtype") || !t.obj.count("shape") || !t.obj.count("data_offsets"))
             return fail(EBH_ERR_SHAPE, ("safetensors: malformed entry " + name).c_str());
-        // Only the encoder's tensors are needed; pooler / classifier / position_ids are skipped.
-        const bool wanted = name.rfind("embeddings.", 0) == 0 || name.rfind("encoder.layer.", 0) == 0;
+        // The encoder's tensors and the cross-encoder head; pooler / position_ids are skipped.
+        const bool wanted = name.rfind("embeddings.", 0) == 0 || name.rfind("encoder.layer.", 0) == 0 ||
+                            name == "classifier.weight" || name == "classifier.bias";
         if (!wanted || name == "embeddings.position_ids") continue;
         const std::string& dt = t.obj.at("dtype").str;
         const JVal& shp = t.obj.at("shape");

@@ -12,6 +12,10 @@ Same entry points and meaning as the Rust API for this path:
 * ``Model.encode(texts, normalize)``          <- ``Model::encode`` (src/lib.rs:479-520),
   including its 1000-entry LRU cache keyed ``"{text}||{normalize}"``; needs
   the HF ``tokenizers`` Tokenizer the reference uses (``tokenizer.json``).
+* ``Model.score_pair(query, document)`` / ``score_batch(pairs)`` <-
+  ``Model::score_pair`` / ``score_batch`` (src/lib.rs:327-383), for models
+  loaded with ``classifier.weight`` / ``classifier.bias``; ``score_ids`` takes
+  pre-tokenised pairs.
 
 Errors raise :class:`EbhError` carrying the C ABI's code and message.
 """
@@ -199,6 +203,47 @@ class Model:
         """``encode_batch`` (src/lib.rs:440-451): one ``encode`` per sub-batch."""
         return [self.encode(b, normalize_embeddings) for b in batches]
 
+    # ---- cross-encoder (score_pair / score_batch) ------------------------
+    def score_ids(self, ids, mask) -> np.ndarray:
+        """Scores of pre-tokenised pairs: u32 ids / mask ``[B, S]``, each row the
+        encoding of one ``"query [SEP] document"`` text -> ``[B]`` (the pooled
+        row ``.dot(classifier.weight) + classifier.bias``, src/lib.rs:359-375)."""
+        ids = np.ascontiguousarray(ids, dtype=np.uint32)
+        mask = np.ascontiguousarray(mask, dtype=np.uint32)
+        if ids.ndim != 2 or mask.shape != ids.shape:
+            raise ValueError("ids and mask must both be [B, S]")
+        B, S = ids.shape
+        out = np.zeros(B, np.float32)
+        N.check(N.lib().ebh_score(self._h, _ptr(ids), _ptr(mask), B, S, _ptr(out)))
+        return out
+
+    def _tokenize_pairs(self, pairs):
+        if self.tokenizer is None:
+            raise RuntimeError("score_pair needs a tokenizer (tokenizer.json); use score_ids")
+        texts = [f"{q} [SEP] {d}" for q, d in pairs]      # src/lib.rs:332
+        encs = self.tokenizer.encode_batch(texts, add_special_tokens=True)
+        S = max(len(e.ids) for e in encs)
+        ids = np.zeros((len(encs), S), np.uint32)
+        mask = np.zeros((len(encs), S), np.uint32)
+        for r, e in enumerate(encs):
+            ids[r, :len(e.ids)] = e.ids
+            mask[r, :len(e.attention_mask)] = e.attention_mask
+        return ids, mask
+
+    def score_pair(self, query: str, document: str) -> float:
+        """``Model::score_pair`` (src/lib.rs:327-376)."""
+        return float(self.score_ids(*self._tokenize_pairs([(query, document)]))[0])
+
+    def score_batch(self, pairs) -> list:
+        """``Model::score_batch`` (src/lib.rs:381-383).  The reference scores the
+        pairs one by one; here they run as one padded batch, which gives each
+        pair the score it gets alone (a pad is a masked key and every other step
+        is per token)."""
+        pairs = list(pairs)
+        if not pairs:
+            return []
+        return [float(x) for x in self.score_ids(*self._tokenize_pairs(pairs))]
+
     # ---- device-resident path (bench / integration) ----------------------
     def encode_device(self, ids_ptr: int, mask_ptr: int, B: int, S: int, out_ptr: int,
                       normalize: bool = True, stream: int | None = None):
@@ -207,6 +252,13 @@ class Model:
                                           ctypes.c_void_p(mask_ptr), B, S, int(bool(normalize)),
                                           ctypes.c_void_p(out_ptr),
                                           ctypes.c_void_p(stream) if stream else None))
+
+    def score_device(self, ids_ptr: int, mask_ptr: int, B: int, S: int, out_ptr: int,
+                     stream: int | None = None):
+        """Enqueue cross-encoder scoring over device buffers (int32 ids / mask, f32 [B] out)."""
+        N.check(N.lib().ebh_score_device(self._h, ctypes.c_void_p(ids_ptr), ctypes.c_void_p(mask_ptr),
+                                         B, S, ctypes.c_void_p(out_ptr),
+                                         ctypes.c_void_p(stream) if stream else None))
 
     def synchronize(self):
         N.check(N.lib().ebh_synchronize(self._h))

@@ -73,13 +73,17 @@ EBH_API int ebh_create(const ebh_config* cfg, ebh_model** out);
  * (src/weights.rs:47-69, src/lib.rs:161-238): hand over one tensor by its HF
  * name.  Data is copied; shape must match the config.  Unknown names fail
  * with EBH_ERR_NOT_FOUND, a wrong rank/shape with EBH_ERR_SHAPE
- * ("Expected 1D tensor ..." as in src/weights.rs:53-57). */
+ * ("Expected 1D tensor ..." as in src/weights.rs:53-57).  The optional
+ * cross-encoder head (src/lib.rs:385-399) is "classifier.weight", [H] or
+ * [1, H], and "classifier.bias" with exactly one value ("Expected scalar"
+ * otherwise, src/weights.rs:99-111). */
 EBH_API int ebh_set_tensor(ebh_model* m, const char* name, const float* data, const int64_t* shape,
                    int32_t ndim);
 
 /* Load every tensor from a model.safetensors file (src/weights.rs:15-45).
- * F32 tensors are read as-is; F16 and BF16 are widened to f32.  Tensors the
- * encoder does not use (pooler.*, classifier.*) are skipped. */
+ * F32 tensors are read as-is; F16 and BF16 are widened to f32.  A
+ * classifier.weight / classifier.bias pair is loaded as the cross-encoder
+ * head; other tensors the encoder does not use (pooler.*) are skipped. */
 EBH_API int ebh_load_safetensors(ebh_model* m, const char* path);
 
 /* End of from_weights: check that every tensor is present (missing ->
@@ -116,6 +120,23 @@ EBH_API int ebh_encode(ebh_model* m, const uint32_t* ids, const uint32_t* mask, 
  * ebh_synchronize().  Successive calls are ordered even across streams. */
 EBH_API int ebh_encode_device(ebh_model* m, const int32_t* ids, const int32_t* mask, int32_t B,
                       int32_t S, int32_t normalize, float* out, void* stream);
+
+/* Cross-encoder scoring (Model::score_pair / score_batch, src/lib.rs:327-383):
+ * each row of ids / mask [B, S] (u32, zero-padded, as ebh_encode) is one
+ * tokenised "query [SEP] document" pair; scores[b] = mean_pool(forward)[b] .
+ * classifier.weight + classifier.bias, without normalisation.  All pairs run
+ * as one batch; a pair's score does not depend on the others (pads are masked
+ * keys and every other step is per token).  Needs a model loaded with
+ * classifier.weight / classifier.bias (else EBH_ERR_STATE "Model is not a
+ * cross-encoder").  Blocking. */
+EBH_API int ebh_score(ebh_model* m, const uint32_t* ids, const uint32_t* mask, int32_t B, int32_t S,
+              float* scores);
+
+/* Device-pointer variant of ebh_score: int32 ids / 0-1 mask [B, S] and
+ * scores [B] in HBM, enqueued on `stream` (NULL = the model's own stream);
+ * returns without waiting, as ebh_encode_device. */
+EBH_API int ebh_score_device(ebh_model* m, const int32_t* ids, const int32_t* mask, int32_t B, int32_t S,
+                     float* scores, void* stream);
 
 /* Wait for the model's outstanding work; EBH_ERR_RANGE if a device-side id
  * check failed since the previous ebh_synchronize / blocking call. */

@@ -51,6 +51,8 @@ def lib():
         L.orc_normalize.argtypes = [_f32p, ctypes.c_int, ctypes.c_int]
         L.orc_cosine_similarity.restype = ctypes.c_float
         L.orc_cosine_similarity.argtypes = [_f32p, _f32p, ctypes.c_int]
+        L.orc_dot.restype = ctypes.c_float
+        L.orc_dot.argtypes = [_f32p, _f32p, ctypes.c_int]
         L.orc_set_num_threads.argtypes = [ctypes.c_int]
         L.orc_get_num_threads.restype = ctypes.c_int
         _LIB = L
@@ -89,6 +91,16 @@ class OracleModel:
     def __init__(self, cfg, weights: dict):
         L = lib()
         self.cfg = cfg
+        # Cross-encoder head (from_cross_encoder_weights, src/lib.rs:385-399):
+        # kept here; the C model holds the encoder.
+        self.classifier = None
+        if "classifier.weight" in weights:
+            w = _f32(weights["classifier.weight"]).reshape(-1)
+            b = _f32(weights["classifier.bias"]).reshape(-1)
+            if w.size != cfg.hidden_size or b.size != 1:
+                raise OracleError("classifier.weight must hold hidden_size values and classifier.bias one")
+            self.classifier = (np.ascontiguousarray(w), np.float32(b[0]))
+        weights = {k: v for k, v in weights.items() if not k.startswith("classifier.")}
         self._h = L.orc_model_new(cfg.hidden_size, cfg.num_attention_heads, cfg.num_hidden_layers,
                                   cfg.intermediate_size, cfg.vocab_size,
                                   cfg.max_position_embeddings, cfg.type_vocab_size,
@@ -129,6 +141,16 @@ class OracleModel:
         if normalize:
             normalize_rows(out)
         return out
+
+    def score(self, input_ids, attention_mask) -> np.ndarray:
+        """``score_pair`` per row (src/lib.rs:327-376): pooled ``forward`` row
+        ``.dot(classifier.weight) + classifier.bias``, in fp32."""
+        if self.classifier is None:
+            raise OracleError("Model is not a cross-encoder")
+        w, b = self.classifier
+        pooled = self.forward(input_ids, attention_mask)
+        return np.array([np.float32(lib().orc_dot(_p(np.ascontiguousarray(r)), _p(w), w.size)) + b
+                         for r in pooled], np.float32)
 
     def encode_unpadded(self, ids, mask, normalize: bool = True) -> np.ndarray:
         """Each sequence run alone at its own length (the padding-free CPU run)."""

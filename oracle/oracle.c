@@ -309,6 +309,25 @@ void orc_normalize(float* x, int B, int H) {
     free(sq);
 }
 
+/* Cross-encoder head (Model::score_pair, src/lib.rs:359-375): the pooled row
+ * (`forward`, not normalised) `.dot(weight) + bias`.  ndarray 0.16's 1-D `dot`
+ * without BLAS is its unrolled_dot: eight partial sums of products, combined
+ * as (p0+p4), (p1+p5), (p2+p6), (p3+p7), then the tail in order -- the shape
+ * of its `sum` above. */
+float orc_dot(const float* a, const float* b, int n) {
+    float p[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    int i = 0;
+    for (; i + 8 <= n; i += 8)
+        for (int j = 0; j < 8; ++j) p[j] = p[j] + a[i + j] * b[i + j];
+    float acc = 0.0f;
+    acc = acc + (p[0] + p[4]);
+    acc = acc + (p[1] + p[5]);
+    acc = acc + (p[2] + p[6]);
+    acc = acc + (p[3] + p[7]);
+    for (; i < n; ++i) acc = acc + a[i] * b[i];
+    return acc;
+}
+
 /* cosine_similarity (src/lib.rs:756-789): eight-wide tree-reduced dot, plain
  * norms, dot / (|a||b| + 1e-8). */
 float orc_cosine_similarity(const float* a, const float* b, int n) {

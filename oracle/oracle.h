@@ -17,6 +17,7 @@
  *   orc_layer_norm       apply_layer_norm_3d        src/lib.rs:980-991
  *   orc_mean_pool        mean_pool                  src/lib.rs:993-1010
  *   orc_normalize        encode_uncached tail       src/lib.rs:605-612
+ *   orc_dot              score_pair head .dot       src/lib.rs:373 (ndarray unrolled_dot)
  *   orc_model_build      Model::from_weights        src/lib.rs:155-260
  *
  * Linear weights are handed over in HF [out,in] layout and transposed at
@@ -68,6 +69,7 @@ void orc_layer_norm(const float* x, int64_t rows, int H, const float* weight, co
 void orc_mean_pool(const float* hidden, const float* mask, int B, int S, int H, float* out);
 void orc_normalize(float* x, int B, int H);
 float orc_cosine_similarity(const float* a, const float* b, int n);
+float orc_dot(const float* a, const float* b, int n);
 
 #ifdef __cplusplus
 }

@@ -13,6 +13,17 @@ def pytest_configure(config):
     config.addinivalue_line("markers", "gpu: runs HIP kernels on an MI355X (cuda:0)")
 
 
+@pytest.fixture(scope="session", autouse=True)
+def _torch_initialises_the_gpu_first(request):
+    """torch ships its own HIP runtime next to the system one the library links;
+    torch finds the GPU only if it initialises the device first.  When any GPU
+    test is selected, let torch do so before any test creates a model."""
+    if any(item.get_closest_marker("gpu") for item in request.session.items):
+        import torch
+        torch.cuda.is_available()
+    yield
+
+
 _WEIGHTS = {}
 
 

@@ -249,6 +249,32 @@ def test_padding_invariance_c2(weights_for):
     np.testing.assert_allclose(padded, alone, rtol=0, atol=2e-6)
 
 
+def test_cross_encoder_head(weights_for):
+    """score_pair's head (src/lib.rs:359-375) on the oracle: with a unit classifier
+    weight e_k the score is exactly pooled[:, k] + bias (every other product is
+    an exact zero); in general it equals the float64 dot of the same pooled rows
+    to fp32 accuracy; a model without the head refuses to score."""
+    cfg = synth.TINY
+    w = dict(weights_for(cfg))
+    ids, mask, _ = _tiny_inputs(B=5)
+    base = oracle.OracleModel(cfg, w)
+    pooled = base.forward(ids.astype(np.float32), mask.astype(np.float32))
+    with pytest.raises(oracle.OracleError):
+        base.score(ids, mask)
+    H = cfg.hidden_size
+    for k in (0, H // 2 + 3, H - 1):
+        e = np.zeros((1, H), np.float32)
+        e[0, k] = 1.0
+        om = oracle.OracleModel(cfg, {**w, "classifier.weight": e,
+                                      "classifier.bias": np.array([0.25], np.float32)})
+        np.testing.assert_array_equal(om.score(ids, mask), pooled[:, k] + np.float32(0.25))
+    cw = (0.02 * np.random.default_rng(0).standard_normal(H)).astype(np.float32)
+    om = oracle.OracleModel(cfg, {**w, "classifier.weight": cw,
+                                  "classifier.bias": np.array([-0.5], np.float32)})
+    want = pooled.astype(np.float64) @ cw.astype(np.float64) - 0.5
+    np.testing.assert_allclose(om.score(ids, mask), want, rtol=0, atol=1e-6)
+
+
 def test_batch_permutation_equivariance(weights_for):
     cfg = synth.TINY
     om = oracle.OracleModel(cfg, weights_for(cfg))
