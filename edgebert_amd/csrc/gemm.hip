@@ -416,16 +416,18 @@ __device__ __forceinline__ int chunk_swizzle16(int r) {
     else return chunk_swizzle<CPR>(r);
 }
 
-// tanh-form GELU of the reference (constants of src/lib.rs:151-152) with
-// tanh(u) = 1 - 2 / (1 + e^(2u)) on the hardware exp2 and reciprocal
-// (|error| of tanh below 2e-7; e^(2u) = inf gives 1, 0 gives -1).
+// tanh-form GELU of the reference (constants of src/lib.rs:151-152),
+// 0.5 x (1 + tanh(u)) with u = sqrt(2/pi) (x + 0.044715 x^3), evaluated as
+// x * sigmoid(2u) = x / (1 + e^(-2u)) on the hardware exp2 and reciprocal:
+// five VALU operations besides those two, and no cancellation for negative x
+// (e^(-2u) = inf gives -0 for finite x; x = +inf gives +inf, -inf gives NaN,
+// as the tanh form does).
 __device__ __forceinline__ float gelu_tanh_fast(float val) {
-    const float SQRT_2_OVER_PI = 0.7978845608f;
-    const float GELU_COEFF = 0.044715f;
-    const float inner = SQRT_2_OVER_PI * (val + GELU_COEFF * (val * val * val));
-    const float e = __builtin_amdgcn_exp2f(inner * 2.8853900817779268f);  // e^(2u)
-    const float t = 1.0f - 2.0f * __builtin_amdgcn_rcpf(1.0f + e);
-    return val * 0.5f * (1.0f + t);
+    // -2 * log2(e) * sqrt(2/pi), and that times 0.044715
+    const float K1 = -2.0f * 1.4426950408889634f * 0.7978845608f;
+    const float K2 = K1 * 0.044715f;
+    const float e = __builtin_amdgcn_exp2f(val * fmaf(val * val, K2, K1));  // e^(-2u)
+    return val * __builtin_amdgcn_rcpf(1.0f + e);
 }
 
 // BF16: A and W are bf16 (16-byte chunk = 8 elements, one
