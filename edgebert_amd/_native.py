@@ -71,6 +71,8 @@ _SIGS = {
     "ebh_op_attention_bf16": (_i32, [_vp, _vp, _i32, _i32, _i32, _i32, _vp, _vp]),
     "ebh_op_layer_norm": (_i32, [_vp, _vp, _vp, _i32, _i32, _f32, _vp, _vp]),
     "ebh_op_add_layer_norm": (_i32, [_vp, _vp, _vp, _vp, _vp, _i32, _i32, _f32, _vp]),
+    "ebh_op_gemm_add_layer_norm": (_i32, [_vp, _i64, _vp, _i64, _vp, _vp, _vp, _vp, _i32, _i32, _i32,
+                                          _f32, _vp]),
     "ebh_op_add_layer_norm_y16": (_i32, [_vp, _vp, _vp, _vp, _vp, _i32, _i32, _f32, _vp]),
     "ebh_op_pool": (_i32, [_vp, _vp, _i32, _i32, _i32, _i32, _vp, _vp]),
     "ebh_op_pack": (_i32, [_vp, _vp, _i32, _i32, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),

@@ -354,6 +354,38 @@ int enqueue_forward(ebh_model* m, const int* d_ids, const int* d_mask, int B, in
         return sp;
     };
     const int sp_out = splits_for(H), sp_down = splits_for(I);
+    // fp32 with at least a 128-row block per CU: the attention-output and
+    // FFN-down products end in their bias + residual + LayerNorm inside the
+    // GEMM (each workgroup holds whole rows), in place on X.
+    const bool fuse_out = !bf16 && ebh::gemm_f32_add_ln_fits(T, H, H);
+    const bool fuse_down = !bf16 && ebh::gemm_f32_add_ln_fits(T, H, I);
+    auto gemm_ln = [&](int kind, const float* A, const float* W, const float* bias, const float* g,
+                       const float* b, int K) -> int {
+        ebh::GemmArgs a{};
+        a.A = A;
+        a.W = W;
+        a.bias = bias;
+        a.R = w.X;
+        a.C = w.X;
+        a.lda = K;
+        a.ldw = K;
+        a.ldr = H;
+        a.ldc = H;
+        a.M_max = T;
+        a.M_dev = w.ntok;
+        a.N = H;
+        a.K = K;
+        a.ln_g = g;
+        a.ln_b = b;
+        a.ln_eps = eps;
+        ProfPair p2{};
+        bool on2 = false;
+        prof_begin(m, kind, s, p2, on2);
+        hipError_t e = ebh::launch_gemm_f32_add_ln(a, s);
+        prof_end(m, s, p2, on2);
+        if (e != hipSuccess) return fail(EBH_ERR_HIP, "gemm launch failed: %s", hipGetErrorString(e));
+        return EBH_OK;
+    };
     for (const DevLayer& L : m->layers) {
         int rc;
         if ((rc = gemm(EBH_PROF_GEMM_QKV, bf16 ? (const void*)w.X16 : w.X, H, L.wqkv, L.wqkv16, L.bqkv,
@@ -365,21 +397,29 @@ int enqueue_forward(ebh_model* m, const int* d_ids, const int* d_mask, int B, in
         else
             HIP_TRY(ebh::launch_attention(w.QKV, w.cu, B, S, H, nh, hd, scale, w.CTX, false, s));
         prof_end(m, s, pp, on);
-        if ((rc = gemm(EBH_PROF_GEMM_OUT, bf16 ? (const void*)ctx16 : w.CTX, H, L.wo, L.wo16, nullptr,
-                       w.Y, H, H, ebh::EPI_NONE, bf16, sp_out)))
-            return rc;
-        prof_begin(m, EBH_PROF_LAYERNORM, s, pp, on);
-        HIP_TRY(add_ln(L.bo, L.ln1_g, L.ln1_b, sp_out));
-        prof_end(m, s, pp, on);
+        if (fuse_out) {
+            if ((rc = gemm_ln(EBH_PROF_GEMM_OUT, w.CTX, L.wo, L.bo, L.ln1_g, L.ln1_b, H))) return rc;
+        } else {
+            if ((rc = gemm(EBH_PROF_GEMM_OUT, bf16 ? (const void*)ctx16 : w.CTX, H, L.wo, L.wo16, nullptr,
+                           w.Y, H, H, ebh::EPI_NONE, bf16, sp_out)))
+                return rc;
+            prof_begin(m, EBH_PROF_LAYERNORM, s, pp, on);
+            HIP_TRY(add_ln(L.bo, L.ln1_g, L.ln1_b, sp_out));
+            prof_end(m, s, pp, on);
+        }
         if ((rc = gemm(EBH_PROF_GEMM_FFN_UP, bf16 ? (const void*)w.X16 : w.X, H, L.w1, L.w116, L.b1,
                        bf16 ? (void*)f16 : (void*)w.F, I, H, ebh::EPI_BIAS_GELU, bf16)))
             return rc;
-        if ((rc = gemm(EBH_PROF_GEMM_FFN_DOWN, bf16 ? (const void*)f16 : w.F, I, L.w2, L.w216, nullptr,
-                       w.Y, H, I, ebh::EPI_NONE, bf16, sp_down)))
-            return rc;
-        prof_begin(m, EBH_PROF_LAYERNORM, s, pp, on);
-        HIP_TRY(add_ln(L.b2, L.ln2_g, L.ln2_b, sp_down));
-        prof_end(m, s, pp, on);
+        if (fuse_down) {
+            if ((rc = gemm_ln(EBH_PROF_GEMM_FFN_DOWN, w.F, L.w2, L.b2, L.ln2_g, L.ln2_b, I))) return rc;
+        } else {
+            if ((rc = gemm(EBH_PROF_GEMM_FFN_DOWN, bf16 ? (const void*)f16 : w.F, I, L.w2, L.w216, nullptr,
+                           w.Y, H, I, ebh::EPI_NONE, bf16, sp_down)))
+                return rc;
+            prof_begin(m, EBH_PROF_LAYERNORM, s, pp, on);
+            HIP_TRY(add_ln(L.b2, L.ln2_g, L.ln2_b, sp_down));
+            prof_end(m, s, pp, on);
+        }
     }
     prof_begin(m, EBH_PROF_POOL, s, pp, on);
     HIP_TRY(ebh::launch_pool(w.X, w.cu, B, H, S, normalize, d_out, s));
@@ -937,6 +977,33 @@ int ebh_op_add_layer_norm(const float* y, const float* bias, float* x, const flo
     if (rows < 0 || H <= 0 || H > 2048) return fail(EBH_ERR_INVALID_ARG, "bad LayerNorm shape");
     HIP_TRY(ebh::launch_add_layernorm(y, bias, x, gamma, beta, rows, nullptr, H, eps, nullptr,
                                       static_cast<hipStream_t>(stream)));
+    return EBH_OK;
+}
+
+int ebh_op_gemm_add_layer_norm(const float* A, int64_t lda, const float* W, int64_t ldw,
+                               const float* bias, float* x, const float* gamma, const float* beta,
+                               int32_t M, int32_t N, int32_t K, float eps, void* stream) {
+    if (!A || !W || !bias || !x || !gamma || !beta) return fail(EBH_ERR_INVALID_ARG, "null buffer");
+    if (M < 0 || N != 384 || K <= 0 || K % 32 || lda < K || ldw < K || lda % 4 || ldw % 4)
+        return fail(EBH_ERR_INVALID_ARG, "bad fused LayerNorm GEMM shape (N must be 384, K %% 32 == 0)");
+    ebh::GemmArgs a{};
+    a.A = A;
+    a.W = W;
+    a.bias = bias;
+    a.R = x;
+    a.C = x;
+    a.lda = lda;
+    a.ldw = ldw;
+    a.ldr = N;
+    a.ldc = N;
+    a.M_max = M;
+    a.M_dev = nullptr;
+    a.N = N;
+    a.K = K;
+    a.ln_g = gamma;
+    a.ln_b = beta;
+    a.ln_eps = eps;
+    HIP_TRY(ebh::launch_gemm_f32_add_ln(a, static_cast<hipStream_t>(stream)));
     return EBH_OK;
 }
 

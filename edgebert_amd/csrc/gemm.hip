@@ -430,6 +430,11 @@ __device__ __forceinline__ float gelu_tanh_fast(float val) {
     return val * __builtin_amdgcn_rcpf(1.0f + e);
 }
 
+// Word 3 of a gfx9 buffer resource descriptor for plain dword-addressed
+// buffers (32-bit data format; no swizzle, no index stride).  Accesses at or
+// past the descriptor's byte count return 0 (loads) or are dropped (stores).
+constexpr int BUFFER_RSRC_WORD3 = 0x00020000;
+
 // BF16: A and W are bf16 (16-byte chunk = 8 elements, one
 // v_mfma_f32_32x32x16_bf16 per fragment pair and k-slice); otherwise fp32
 // (chunk = 4 elements, four v_mfma_f32_32x32x2_f32).  OUT16: C is written as
@@ -440,7 +445,10 @@ template <bool BF16, bool OUT16, int BM, int BN, int BK, int WAVES_M, int WAVES_
 __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_persistent_kernel(GemmArgs p) {
     constexpr int ES = BF16 ? 2 : 4;              // bytes per element
     constexpr int EPC = 16 / ES;                  // elements per 16-byte chunk
-    static_assert(EPI == EPI_BIAS || EPI == EPI_BIAS_GELU || EPI == EPI_NONE, "no residual here");
+    static_assert(EPI == EPI_BIAS || EPI == EPI_BIAS_GELU || EPI == EPI_NONE || EPI == EPI_ADD_LN,
+                  "no plain residual here");
+    constexpr bool LN = EPI == EPI_ADD_LN;
+    static_assert(!LN || (!BF16 && !OUT16 && BM / WAVES_M == 64), "LayerNorm epilogue: fp32, 64-row wave tiles");
     constexpr bool HAS_BIAS = EPI != EPI_NONE;
     constexpr int NT = 64 * WAVES_M * WAVES_N, NW = WAVES_M * WAVES_N;
     constexpr int WM = BM / WAVES_M, WN = BN / WAVES_N;
@@ -454,10 +462,11 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_persistent_kernel
     constexpr int LA = A_CH / NT, LW = W_CH / NT, NL = LA + LW;
     constexpr int D = NSTAGE - 1;                 // k-tiles in flight ahead
     constexpr int STAGE = (BM + BN) * RW;         // words per stage: A rows, then W rows
-    static_assert(NW * 32 * WN <= STAGE, "each wave transposes 32 C rows at a time through one stage");
+    static_assert(LN || NW * 32 * WN <= STAGE, "each wave transposes 32 C rows at a time through one stage");
+    static_assert(!LN || 2 * WAVES_N * BM + 2 * NW * 64 <= STAGE, "LayerNorm exchange fits one stage");
     constexpr int C4 = WN / 4;                    // float4 per wave-tile row
     constexpr int RPP = 64 / C4;                  // wave-tile rows per float4 pass
-    static_assert(C4 * RPP == 64 && 32 % RPP == 0, "epilogue pass shape");
+    static_assert(LN || (C4 * RPP == 64 && 32 % RPP == 0), "epilogue pass shape");
     constexpr int NPB = 32 / RPP;                 // float4 passes per 32-row block
     constexpr int BIAS_SLOT = 256;                // floats: one wave's 64 x 16-byte bias chunks
 
@@ -552,6 +561,144 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_persistent_kernel
     const int e_r = lane / C4, e_c = 4 * (lane % C4);
 
     v16f acc[FM][FN];
+
+    // EPI_ADD_LN: the tile spans whole rows (one tile column), so the workgroup
+    // holds every value of its rows.  Lane (l32, half) of wave (wm, wn) holds,
+    // in acc[i][j][r], row wm*64 + i*32 + 8*(r/4) + 4*half + r%4 of the tile at
+    // column wn*WN + j*32 + l32; a row's values lie in the 32 lanes of one
+    // half-wave (3 each here) and in the WAVES_N waves of one wave row.
+    //
+    // Sum of each of this lane's 32 row values q[i*16 + r] over the 32 lanes of
+    // its half-wave by recursive halving: at each step a lane keeps the half of
+    // its values that its lane bit selects, each plus its partner's copy, so
+    // lane l32 ends with the total of value l32.  (Both halves are exchanged and
+    // the choice is made between the sums: a choice between two elements of q
+    // would index q by lane and keep it out of registers.)
+    auto half_wave_sums = [&](float (&q)[32]) __attribute__((always_inline)) -> float {
+#pragma unroll
+        for (int step = 0; step < 5; ++step) {
+            const int m = 16 >> step;
+            const bool up = (l32 & m) != 0;
+#pragma unroll
+            for (int k = 0; k < m; ++k) {
+                const float lo = q[k] + __shfl_xor(q[k], m);
+                const float hi = q[k + m] + __shfl_xor(q[k + m], m);
+                q[k] = up ? hi : lo;
+            }
+        }
+        return q[0];
+    };
+    // Row index within the wave tile of value v = i*16 + r (held by lane l32 = v
+    // after half_wave_sums).
+    const int my_row = (l32 >> 4) * 32 + 8 * ((l32 & 15) >> 2) + 4 * half + (l32 & 3);
+    // Row totals across the WAVES_N waves of a wave row, through LDS `red`
+    // ([WAVES_N][BM]); then each lane's statistic for its own row is handed to
+    // the lanes holding the row's values through the wave's slot of `bc`
+    // ([NW][64]) and read back as v[i][r].
+    auto row_stat = [&](float part, float* red, float* bc, auto&& finish, float (&v)[FM][16])
+                        __attribute__((always_inline)) {
+        red[wn * BM + wm * WM + my_row] = part;
+        lds_barrier();
+        float tot = red[wm * WM + my_row];
+#pragma unroll
+        for (int w = 1; w < WAVES_N; ++w) tot += red[w * BM + wm * WM + my_row];
+        bc[wave * 64 + my_row] = finish(tot);
+#pragma unroll
+        for (int i = 0; i < FM; ++i)
+#pragma unroll
+            for (int g4 = 0; g4 < 4; ++g4) {
+                const float4 f = *reinterpret_cast<const float4*>(bc + wave * 64 + i * 32 + 8 * g4 + 4 * half);
+                v[i][4 * g4] = f.x; v[i][4 * g4 + 1] = f.y; v[i][4 * g4 + 2] = f.z; v[i][4 * g4 + 3] = f.w;
+            }
+    };
+    // x = LayerNorm((acc + bias) + R) for local tile t, in the order of the
+    // unfused add-LayerNorm: mean, then the mean of squared deviations, then
+    // (v - mean) * (1 / sqrt(var + eps)) * gamma + beta.  `ex` is a consumed
+    // LDS stage (the exchange buffers).
+    auto epilogue_ln = [&](int t, float* ex) __attribute__((always_inline)) {
+        const int m0 = (wg + t * G) * BM;
+        const float* bsl = smem + NSTAGE * STAGE + ((t & 1) * NW + wave) * BIAS_SLOT + l32;
+        const int col = wn * WN + l32;
+        // R and C are [M, BN] (row stride BN), read and written through buffer
+        // descriptors that start at the tile's first row and end at row M.
+        // Element (i, j, r) of this lane lies lane_off + 128 j bytes (the
+        // lane's part) plus row_off(i, r) bytes (uniform: the scalar offset)
+        // from the tile start; a row at or past M gets a lane offset past the
+        // descriptor's end, so it reads 0 and is not written.
+        const int valid = min(M - m0, BM);
+        const __amdgpu_buffer_rsrc_t rx = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<float*>(p.R) + (int64_t)m0 * BN, (short)0, valid * BN * 4, BUFFER_RSRC_WORD3);
+        const __amdgpu_buffer_rsrc_t cx = __builtin_amdgcn_make_buffer_rsrc(
+            p.C + (int64_t)m0 * BN, (short)0, valid * BN * 4, BUFFER_RSRC_WORD3);
+        const int lane_row = wm * WM + 4 * half;
+        int lane_off = (lane_row * BN + col) * 4;
+        // Opaque per tile: keeps the 96 offsets derived from it from being
+        // computed once ahead of the tile loop and held in registers.
+        asm volatile("" : "+v"(lane_off));
+        auto row_c = [](int i, int r) { return i * 32 + 8 * (r >> 2) + (r & 3); };
+        const int lim = valid - lane_row;         // rows row_c < lim of this lane are real
+        auto voff = [&](int i, int r) { return row_c(i, r) < lim ? lane_off : (int)0x80000000; };
+        float bj[FN], gj[FN], betaj[FN];
+#pragma unroll
+        for (int j = 0; j < FN; ++j) {
+            bj[j] = bsl[j * 32];
+            gj[j] = p.ln_g[col + j * 32];
+            betaj[j] = p.ln_b[col + j * 32];
+        }
+        // The residual loads go out one 32-row block at a time (48 registers in
+        // flight beside the 96 accumulators).
+#pragma unroll
+        for (int i = 0; i < FM; ++i) {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int vo = voff(i, r), so = row_c(i, r) * BN * 4;
+#pragma unroll
+                for (int j = 0; j < FN; ++j)
+                    acc[i][j][r] = (acc[i][j][r] + bj[j]) +
+                                   __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rx, vo + 128 * j, so, 0));
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        float q[32], st[FM][16];
+#pragma unroll
+        for (int i = 0; i < FM; ++i)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                float sum = acc[i][0][r];
+#pragma unroll
+                for (int j = 1; j < FN; ++j) sum += acc[i][j][r];
+                q[i * 16 + r] = sum;
+            }
+        const float inv_n = 1.0f / (float)N;
+        row_stat(half_wave_sums(q), ex, ex + 2 * WAVES_N * BM, [&](float tot) { return tot * inv_n; }, st);
+#pragma unroll
+        for (int i = 0; i < FM; ++i)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                float sum = 0.0f;
+#pragma unroll
+                for (int j = 0; j < FN; ++j) {
+                    const float d = acc[i][j][r] - st[i][r];
+                    acc[i][j][r] = d;
+                    sum += d * d;
+                }
+                q[i * 16 + r] = sum;
+            }
+        const float eps = p.ln_eps;
+        row_stat(half_wave_sums(q), ex + WAVES_N * BM, ex + 2 * WAVES_N * BM + NW * 64,
+                 [&](float tot) { return 1.0f / sqrtf(tot * inv_n + eps); }, st);
+#pragma unroll
+        for (int i = 0; i < FM; ++i)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int vo = voff(i, r), so = row_c(i, r) * BN * 4;
+#pragma unroll
+                for (int j = 0; j < FN; ++j)
+                    __builtin_amdgcn_raw_buffer_store_b32(
+                        __float_as_uint(acc[i][j][r] * st[i][r] * gj[j] + betaj[j]), cx, vo + 128 * j, so, 0);
+            }
+    };
+
     // Epilogue of local tile t: bias (+ GELU), C through LDS stage `cs`, float4 stores.
     auto epilogue_tile = [&](int t, const float* cs_base) {
         const int u = wg + t * G, split = u / ntiles, tile = u - split * ntiles;
@@ -594,6 +741,11 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_persistent_kernel
         }
     };
 
+    auto finish_tile = [&](int t, float* stage) __attribute__((always_inline)) {
+        if constexpr (LN) epilogue_ln(t, stage);
+        else epilogue_tile(t, stage);
+    };
+
     point_at(0);
 #pragma unroll
     for (int d = 0; d < D; ++d)
@@ -607,8 +759,8 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_persistent_kernel
             wait_vmcnt(after);
             lds_barrier();
             if (kt == 0) {
-                if (t > 0) {
-                    epilogue_tile(t - 1, smem + ((it - 1) % NSTAGE) * STAGE);
+                if (!LN && t > 0) {
+                    finish_tile(t - 1, smem + ((it - 1) % NSTAGE) * STAGE);
                     lds_barrier();  // the stage is refilled by the loads below
                 }
 #pragma unroll
@@ -651,9 +803,18 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_persistent_kernel
                 }
             }
         }
+        // EPI_ADD_LN: one epilogue site, at the end of each tile (the next
+        // tile's first k-tile is already on its way into the other stage).
+        if constexpr (LN) {
+            lds_barrier();  // every wave is done with this tile's last stage
+            finish_tile(t, smem + ((it - 1) % NSTAGE) * STAGE);
+            lds_barrier();  // that stage is refilled next
+        }
     }
-    lds_barrier();  // every wave is done with the last k-tile's stage
-    epilogue_tile(my_tiles - 1, smem + ((it - 1) % NSTAGE) * STAGE);
+    if constexpr (!LN) {
+        lds_barrier();  // every wave is done with the last k-tile's stage
+        finish_tile(my_tiles - 1, smem + ((it - 1) % NSTAGE) * STAGE);
+    }
 }
 
 // ---------------------------------------------------------------------------
@@ -923,6 +1084,34 @@ int gemm_f32_splits(int M_max, int N, int K) {
     for (int S : {4, 2})
         if (K % (64 * S) == 0 && K / S >= 128) return S;
     return 1;
+}
+
+// Fused projection + bias + residual + LayerNorm: 128 x 384 tiles (whole rows
+// of a 384-wide output), 32-deep k-tiles, 8 waves of 64 x 96, two LDS stages
+// (2 x 64 KB) plus the bias slots, one workgroup per CU.  Measured on MI355X
+// at 32k tokens of MiniLM width, this tile's main loop runs the attention-output
+// and FFN-down products faster than 128 x 128 tiles do, and the LayerNorm pass
+// that would follow (a read of the product and the residual, a write of x) is
+// gone; with fewer row blocks than CUs part of the chip would idle, so the
+// split 128 x 128 path and its separate LayerNorm stay the choice there.
+constexpr int ADD_LN_BM = 128, ADD_LN_BN = 384, ADD_LN_BK = 32;
+
+bool gemm_f32_add_ln_fits(int M_max, int N, int K) {
+    return N == ADD_LN_BN && K % ADD_LN_BK == 0 && K >= ADD_LN_BK &&
+           (M_max + ADD_LN_BM - 1) / ADD_LN_BM >= cu_count();
+}
+
+hipError_t launch_gemm_f32_add_ln(const GemmArgs& a, hipStream_t s) {
+    const bool ok = a.N == ADD_LN_BN && a.K % ADD_LN_BK == 0 && a.K >= ADD_LN_BK && a.splits <= 1 &&
+                    aligned16(a.A) && aligned16(a.W) && aligned16(a.bias) && a.R && a.C && a.ln_g &&
+                    a.ln_b && a.lda % 4 == 0 && a.ldw % 4 == 0 && a.M_max >= 0;
+    if (!ok) return hipErrorInvalidValue;
+    const int tiles = (a.M_max + ADD_LN_BM - 1) / ADD_LN_BM;
+    if (tiles == 0) return hipSuccess;
+    const int grid = std::min(tiles, cu_count());
+    hipLaunchKernelGGL((gemm_persistent_kernel<false, false, ADD_LN_BM, ADD_LN_BN, ADD_LN_BK, 2, 4, 2, EPI_ADD_LN>),
+                       dim3(grid), dim3(512), 0, s, a);
+    return hipGetLastError();
 }
 
 // bf16 activations: 256 x 256 tiles, 64-deep k-tiles (8 chunks of 8), 8 waves

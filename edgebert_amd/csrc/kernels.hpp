@@ -7,8 +7,9 @@ namespace ebh {
 
 // GEMM epilogues: bias, then optionally GELU (FFN up) or a residual add; or
 // none at all (the forward adds bias and residual of the attention-output and
-// FFN-down projections in the LayerNorm that follows them).
-enum Epilogue : int { EPI_BIAS = 0, EPI_BIAS_GELU = 1, EPI_BIAS_RESID = 2, EPI_NONE = 3 };
+// FFN-down projections in the LayerNorm that follows them); or bias, residual
+// and that LayerNorm in one (EPI_ADD_LN, launch_gemm_f32_add_ln).
+enum Epilogue : int { EPI_BIAS = 0, EPI_BIAS_GELU = 1, EPI_BIAS_RESID = 2, EPI_NONE = 3, EPI_ADD_LN = 4 };
 
 struct GemmArgs {
     const void* A;       // [M, K] row-major activations (fp32)
@@ -24,6 +25,10 @@ struct GemmArgs {
     // [s*K/splits, (s+1)*K/splits) into C + s * split_stride.
     int splits;
     int64_t split_stride;
+    // EPI_ADD_LN: LayerNorm gamma / beta [N] and epsilon.
+    const float* ln_g;
+    const float* ln_b;
+    float ln_eps;
 };
 
 // Split count launch_gemm_f32 takes best for a bias-free product of this shape
@@ -47,6 +52,14 @@ hipError_t launch_attention(const float* qkv, const int* cu_seqlens, int B, int 
 hipError_t launch_attention_bf16(const uint16_t* qkv, const int* cu_seqlens, int B, int max_len,
                                  int H, int nh, int head_dim, float scale, uint16_t* ctx,
                                  hipStream_t s);
+
+// C = LayerNorm((A . W^T + bias) + R) per row (fp32), C may alias R (each
+// element is read and written by the same lane).  One workgroup owns whole rows
+// (128 x 384 tiles), so it takes N == 384; gemm_f32_add_ln_fits tells whether
+// this fused form is the faster one for the shape (enough rows to give every CU
+// a tile).  hipErrorInvalidValue for shapes or alignments it does not take.
+bool gemm_f32_add_ln_fits(int M_max, int N, int K);
+hipError_t launch_gemm_f32_add_ln(const GemmArgs& a, hipStream_t s);
 
 // bf16 activations and weights, fp32 accumulate: C = epi(A . W^T + bias), A [M,K]
 // and W [N,K] bf16 bits, C fp32 or (c_bf16) bf16 bits.  Needs 16-byte aligned

@@ -73,6 +73,18 @@ EBH_API int ebh_op_layer_norm(const float* x, const float* gamma, const float* b
 EBH_API int ebh_op_add_layer_norm(const float* y, const float* bias, float* x, const float* gamma,
                           const float* beta, int32_t rows, int32_t H, float eps, void* stream);
 
+/* A residual block's projection and end in one kernel (src/lib.rs:672-674,
+ * 677-679 with the Linear of 732-733 / 741-747): x = LayerNorm((A.W^T + bias)
+ * + x), in place on x [M, N] (row stride N), A [M, K] fp32 (lda), W [N, K] fp32
+ * (ldw).  Each 128-row block is one workgroup that holds whole rows, so N must
+ * be 384 (the MiniLM width); K % 32 == 0, strides multiples of 4, A, W and
+ * bias 16-byte aligned.  Same result, within fp32 rounding, as ebh_op_gemm
+ * (EBH_EPI_NONE) followed by ebh_op_add_layer_norm; the fp32 forward uses it
+ * when there are at least as many 128-row blocks as CUs. */
+EBH_API int ebh_op_gemm_add_layer_norm(const float* A, int64_t lda, const float* W, int64_t ldw,
+                               const float* bias, float* x, const float* gamma, const float* beta,
+                               int32_t M, int32_t N, int32_t K, float eps, void* stream);
+
 /* The same with y stored as bf16 (the projections of bf16 models); the sums,
  * statistics and x stay fp32.  y rows 8-byte aligned, the fp32 operands
  * 16-byte aligned, and H = 4 * L * n with L in {64, 32, 16}, n in

@@ -301,6 +301,54 @@ def test_add_layer_norm(env, H):
     np.testing.assert_allclose(dx.cpu().numpy(), want, rtol=0, atol=1e-5)
 
 
+@pytest.mark.parametrize("M,K", [
+    (32768, 384),     # attention-output shape at 256 x 128 tokens: one row block per CU
+    (32768, 1536),    # FFN-down shape
+    (33000, 384),     # more row blocks than CUs: a second round and a ragged last block
+    (1000, 1536),     # few rows (the op takes any M; the forward would not fuse here)
+    (5, 64),
+])
+def test_gemm_add_layer_norm(env, M, K):
+    """x = LN((A.W^T + b) + x) in one kernel: against the float64 product and
+    LayerNorm, and against the unfused GEMM + add-LayerNorm pair on the GPU."""
+    torch, eb, Nn, L = env
+    rng = np.random.default_rng(M + K)
+    H = 384
+    A = rng.standard_normal((M, K)).astype(np.float32)
+    W = (rng.standard_normal((H, K)) / np.sqrt(K)).astype(np.float32)
+    b = rng.standard_normal(H).astype(np.float32)
+    x = rng.standard_normal((M, H)).astype(np.float32)
+    g = rng.standard_normal(H).astype(np.float32)
+    beta = rng.standard_normal(H).astype(np.float32)
+    dA, dW, db, dg, dbeta = (dev(torch, a) for a in (A, W, b, g, beta))
+    dx, dx2 = dev(torch, x), dev(torch, x)
+    eps = ctypes.c_float(1e-12)
+    Nn.check(L.ebh_op_gemm_add_layer_norm(vp(dA), K, vp(dW), K, vp(db), vp(dx), vp(dg), vp(dbeta),
+                                          M, H, K, eps, stream(torch)))
+    dy = torch.empty((M, H), device="cuda")
+    Nn.check(L.ebh_op_gemm(vp(dA), K, vp(dW), K, Nn.EBH_DTYPE_F32, None, None, H, vp(dy), H, M, H, K, 3,
+                           stream(torch)))
+    Nn.check(L.ebh_op_add_layer_norm(vp(dy), vp(db), vp(dx2), vp(dg), vp(dbeta), M, H, eps, stream(torch)))
+    torch.cuda.synchronize()
+    v = (A.astype(np.float64) @ W.T.astype(np.float64) + b) + x
+    mu = v.mean(1, keepdims=True)
+    var = ((v - mu) ** 2).mean(1, keepdims=True)
+    want = (v - mu) / np.sqrt(var + 1e-12) * g + beta
+    got = dx.cpu().numpy()
+    # v has unit-order spread per row; fp32 GEMM and statistics errors reach
+    # the output scaled by |gamma| (up to about 4 here).
+    np.testing.assert_allclose(got, want, rtol=0, atol=5e-5)
+    np.testing.assert_allclose(got, dx2.cpu().numpy(), rtol=0, atol=5e-5)
+
+
+def test_gemm_add_layer_norm_rejects_other_widths(env):
+    torch, eb, Nn, L = env
+    t = torch.zeros(1024, device="cuda")
+    rc = L.ebh_op_gemm_add_layer_norm(vp(t), 64, vp(t), 64, vp(t), vp(t), vp(t), vp(t), 2, 8, 64,
+                                      ctypes.c_float(1e-12), stream(torch))
+    assert rc == Nn.EBH_ERR_INVALID_ARG
+
+
 @pytest.mark.parametrize("H", [384, 768])
 def test_add_layer_norm_bf16_projection(env, H):
     """The same block end with y held as bf16 (bf16 models): equal to the fp32
