@@ -13,7 +13,13 @@ there is one.  ``cpu_baseline`` times the repo's C restatement of the
 reference CPU path (``oracle/``) on a bounded sample of the same workload on
 this host.  ``host_api`` is the rate of the blocking host-buffer entry point
 (``ebh_encode``: ids / mask copied in over PCIe, vectors copied back); it is
-reported beside ``value``, never as it.
+reported beside ``value``, never as it.  ``encode_texts`` is the rate from
+texts (``Model::encode`` without its cache): the native tokenizer on host
+threads writing into the pinned staging buffers, then the same forward; the
+texts are the workload's ids spelled as words of a synthetic vocabulary, so
+they tokenise back to exactly those ids (``matches_ids``).  Beside it, the
+tokenisation alone, native and with the HF ``tokenizers`` library the
+reference uses.
 """
 from __future__ import annotations
 
@@ -110,6 +116,44 @@ def cpu_baseline(spec, weights, ids, mask, budget_s: float):
                       f"{oracle.get_num_threads()} OpenMP threads of {os.cpu_count()} host CPUs"}
 
 
+def text_path(model, spec, ids, mask, lengths, steps: int) -> dict:
+    """Texts -> vectors through ebh_encode_texts, and the tokenisers alone."""
+    from edgebert_amd import synth
+    from edgebert_amd.tokenizer import Tokenizer, hf_tokenizer_from_str
+
+    doc = synth.tokenizer_json(spec.model)
+    tok = Tokenizer.from_str(doc)
+    texts = synth.make_texts(ids, lengths)
+    B = len(texts)
+    model.tokenizer = tok
+    ref = model.encode_ids(ids, mask, normalize=True)
+    got = model.encode_texts(texts, True)
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        model.encode_texts(texts, True)
+    el = time.perf_counter() - t0
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        tok.encode_batch_ids(texts)
+    el_tok = time.perf_counter() - t0
+    out = {"value": round(B * steps / el, 2), "unit": "sentences/s",
+           "matches_ids": bool(np.array_equal(got, ref)),
+           "tokenize_native": round(B * steps / el_tok, 2),
+           "threads": min(16, os.cpu_count() or 1)}
+    try:
+        hf = hf_tokenizer_from_str(doc)
+        hf.encode_batch(texts, add_special_tokens=True)
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            hf.encode_batch(texts, add_special_tokens=True)
+        out["tokenize_hf_tokenizers"] = round(B * steps / (time.perf_counter() - t0), 2)
+    except ImportError:
+        out["tokenize_hf_tokenizers"] = None
+    out["note"] = ("ebh_encode_texts: native tokenizer on host threads into pinned staging + H2D + "
+                   "forward + D2H; tokenize_*: encode_batch alone")
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -122,6 +166,8 @@ def main():
                     help="seconds of CPU baseline work (0 disables)")
     ap.add_argument("--host-api-steps", type=int, default=5,
                     help="blocking host-buffer forwards timed for host_api (0 disables)")
+    ap.add_argument("--text-steps", type=int, default=5,
+                    help="batches timed for encode_texts and the tokenizers (0 disables)")
     ap.add_argument("--copy-probe-mb", type=int, default=0,
                     help="after the timed region, run 3 plain device copies of this many MiB "
                          "(the calibration dispatch for rocprofv3 FETCH_SIZE / WRITE_SIZE)")
@@ -221,6 +267,8 @@ def main():
         result["host_api"] = {"value": round(B * args.host_api_steps / el, 2),
                               "unit": "sentences/s",
                               "note": "ebh_encode on host buffers: validation + H2D + forward + D2H"}
+    if args.text_steps > 0:
+        result["encode_texts"] = text_path(model, spec, ids, mask, lengths, args.text_steps)
     if args.copy_probe_mb > 0:
         n = args.copy_probe_mb * (1 << 20) // 4
         src = torch.ones(n, dtype=torch.float32, device=dev)

@@ -9,6 +9,8 @@ library every entry point raises.
 from .synth import BertConfig, MINILM_L6, BERT_BASE, TINY, CONFIGS, make_weights, make_inputs
 from ._native import EbhError, lib, header_symbols
 from .model import Model, cosine_similarity
+from .tokenizer import Tokenizer
 
 __all__ = ["BertConfig", "MINILM_L6", "BERT_BASE", "TINY", "CONFIGS", "make_weights",
-           "make_inputs", "EbhError", "lib", "header_symbols", "Model", "cosine_similarity"]
+           "make_inputs", "EbhError", "lib", "header_symbols", "Model", "cosine_similarity",
+           "Tokenizer"]

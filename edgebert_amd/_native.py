@@ -59,6 +59,12 @@ _SIGS = {
     "ebh_score": (_i32, [_vp, _vp, _vp, _i32, _i32, _vp]),
     "ebh_score_device": (_i32, [_vp, _vp, _vp, _i32, _i32, _vp, _vp]),
     "ebh_synchronize": (_i32, [_vp]),
+    "ebh_tokenizer_load": (_i32, [ctypes.c_char_p, ctypes.POINTER(_vp)]),
+    "ebh_tokenizer_from_json": (_i32, [ctypes.c_char_p, ctypes.c_size_t, ctypes.POINTER(_vp)]),
+    "ebh_tokenizer_destroy": (None, [_vp]),
+    "ebh_tokenize": (_i32, [_vp, _vp, _vp, _i32, _i32, _vp, _vp, ctypes.POINTER(_i32), _i32]),
+    "ebh_encode_texts": (_i32, [_vp, _vp, _vp, _vp, _i32, _i32, _vp, _i32]),
+    "ebh_score_texts": (_i32, [_vp, _vp, _vp, _vp, _vp, _vp, _i32, _vp, _i32]),
     "ebh_last_tokens": (_i32, [_vp, _vp, _vp, _i64, _vp, _i64, _vp]),
     "ebh_model_info": (_i32, [_vp, ctypes.POINTER(EbhConfig), ctypes.POINTER(_i32)]),
     "ebh_profile_enable": (_i32, [_vp, _i32]),

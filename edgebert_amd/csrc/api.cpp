@@ -784,6 +784,59 @@ int ebh_score(ebh_model* m, const uint32_t* ids, const uint32_t* mask, int32_t B
     return forward_host_staged(m, B, S, 0, scores, true);
 }
 
+// Tokenised texts (host threads, outside the model's lock) -> pinned staging -> forward.
+static int forward_texts(ebh_model* m, const ebh_tokenizer* t, const char* const* texts, const int64_t* lens,
+                         int32_t n, int32_t normalize, float* out, int32_t nthreads, bool score) {
+    int rc = check_model_ready(m);
+    if (rc) return rc;
+    if (score && !m->cross_encoder) return fail(EBH_ERR_STATE, "Model is not a cross-encoder");
+    if (!t) return fail(EBH_ERR_INVALID_ARG, "null tokenizer");
+    if (n < 0) return fail(EBH_ERR_INVALID_ARG, "negative batch");
+    if (n == 0) return EBH_OK;
+    if (!texts || !out) return fail(EBH_ERR_INVALID_ARG, "null buffer");
+    std::vector<std::vector<int32_t>> seqs;
+    int S = 0;
+    if ((rc = ebh::tokenize_batch(t, texts, lens, n, nthreads, seqs, &S))) return rc;
+    if ((rc = check_dims(m, n, S))) return rc;
+    const int H = m->cfg.hidden_size;
+    std::lock_guard<std::mutex> lk(m->mu);
+    HIP_TRY(hipSetDevice(m->device));
+    const int64_t T = (int64_t)n * S;
+    if ((rc = ensure_host_staging(m, T, (int64_t)n * H))) return rc;
+    ebh::write_padded(t, seqs, S, m->h_ids, m->h_mask);
+    for (int64_t i = 0; i < T; ++i)
+        if (m->h_ids[i] < 0 || m->h_ids[i] >= m->cfg.vocab_size)
+            return fail(EBH_ERR_RANGE, "token id %d at [%lld, %lld] out of range for vocab %d", m->h_ids[i],
+                        (long long)(i / S), (long long)(i % S), m->cfg.vocab_size);
+    return forward_host_staged(m, n, S, normalize ? 1 : 0, out, score);
+}
+
+int ebh_encode_texts(ebh_model* m, const ebh_tokenizer* t, const char* const* texts, const int64_t* lens,
+                     int32_t n, int32_t normalize, float* out, int32_t nthreads) {
+    return forward_texts(m, t, texts, lens, n, normalize, out, nthreads, false);
+}
+
+int ebh_score_texts(ebh_model* m, const ebh_tokenizer* t, const char* const* queries, const int64_t* q_lens,
+                    const char* const* documents, const int64_t* d_lens, int32_t n, float* scores,
+                    int32_t nthreads) {
+    if (n > 0 && (!queries || !documents)) return fail(EBH_ERR_INVALID_ARG, "null buffer");
+    std::vector<std::string> pairs(n > 0 ? n : 0);
+    std::vector<const char*> ptrs(pairs.size());
+    std::vector<int64_t> lens(pairs.size());
+    for (int32_t i = 0; i < n; ++i) {
+        const int64_t ql = q_lens ? q_lens[i] : (queries[i] ? (int64_t)strlen(queries[i]) : -1);
+        const int64_t dl = d_lens ? d_lens[i] : (documents[i] ? (int64_t)strlen(documents[i]) : -1);
+        if (ql < 0 || dl < 0 || (ql && !queries[i]) || (dl && !documents[i]))
+            return fail(EBH_ERR_INVALID_ARG, "null text or negative length at %d", i);
+        pairs[i].assign(queries[i] ? queries[i] : "", ql);   // "{query} [SEP] {document}", src/lib.rs:331
+        pairs[i] += " [SEP] ";
+        pairs[i].append(documents[i] ? documents[i] : "", dl);
+        ptrs[i] = pairs[i].data();
+        lens[i] = (int64_t)pairs[i].size();
+    }
+    return forward_texts(m, t, ptrs.data(), lens.data(), n, 0, scores, nthreads, true);
+}
+
 int ebh_score_device(ebh_model* m, const int32_t* ids, const int32_t* mask, int32_t B, int32_t S,
                      float* scores, void* stream) {
     int rc = check_model_ready(m);

@@ -18,125 +18,13 @@
 
 #include "../../include/edgebert_hip.h"
 #include "internal.hpp"
+#include "json.hpp"
 
 namespace {
 
-struct JVal {
-    enum Kind { NUL, BOOL, NUM, STR, ARR, OBJ } kind = NUL;
-    double num = 0;
-    std::string str;
-    std::vector<JVal> arr;
-    std::map<std::string, JVal> obj;
-};
+using ebh::json::JVal;
+using ebh::json::Parser;
 
-struct Parser {
-    const char* p;
-    const char* end;
-    std::string err;
-
-    void ws() {
-        while (p < end && (*p == ' ' || *p == '\n' || *p == '\r' || *p == '\t')) ++p;
-    }
-    bool expect(char c) {
-        ws();
-        if (p < end && *p == c) { ++p; return true; }
-        err = std::string("expected '") + c + "'";
-        return false;
-    }
-    bool parse_string(std::string& out) {
-        if (!expect('"')) return false;
-        while (p < end && *p != '"') {
-            char c = *p++;
-            if (c == '\\') {
-                if (p >= end) break;
-                char e = *p++;
-                switch (e) {
-                    case '"': out += '"'; break;
-                    case '\\': out += '\\'; break;
-                    case '/': out += '/'; break;
-                    case 'b': out += '\b'; break;
-                    case 'f': out += '\f'; break;
-                    case 'n': out += '\n'; break;
-                    case 'r': out += '\r'; break;
-                    case 't': out += '\t'; break;
-                    case 'u': {
-                        if (end - p < 4) { err = "bad \\u escape"; return false; }
-                        unsigned cp = 0;
-                        for (int i = 0; i < 4; ++i) {
-                            char h = *p++;
-                            cp <<= 4;
-                            if (h >= '0' && h <= '9') cp |= h - '0';
-                            else if (h >= 'a' && h <= 'f') cp |= h - 'a' + 10;
-                            else if (h >= 'A' && h <= 'F') cp |= h - 'A' + 10;
-                            else { err = "bad \\u escape"; return false; }
-                        }
-                        if (cp < 0x80) out += (char)cp;
-                        else if (cp < 0x800) { out += (char)(0xC0 | (cp >> 6)); out += (char)(0x80 | (cp & 0x3F)); }
-                        else { out += (char)(0xE0 | (cp >> 12)); out += (char)(0x80 | ((cp >> 6) & 0x3F)); out += (char)(0x80 | (cp & 0x3F)); }
-                        break;
-                    }
-                    default: err = "bad escape"; return false;
-                }
-            } else {
-                out += c;
-            }
-        }
-        if (p >= end) { err = "unterminated string"; return false; }
-        ++p;
-        return true;
-    }
-    bool parse(JVal& v, int depth = 0) {
-        if (depth > 64) { err = "nesting too deep"; return false; }
-        ws();
-        if (p >= end) { err = "unexpected end"; return false; }
-        char c = *p;
-        if (c == '{') {
-            ++p;
-            v.kind = JVal::OBJ;
-            ws();
-            if (p < end && *p == '}') { ++p; return true; }
-            while (true) {
-                std::string key;
-                if (!parse_string(key)) return false;
-                if (!expect(':')) return false;
-                JVal child;
-                if (!parse(child, depth + 1)) return false;
-                v.obj[key] = std::move(child);
-                ws();
-                if (p < end && *p == ',') { ++p; continue; }
-                return expect('}');
-            }
-        }
-        if (c == '[') {
-            ++p;
-            v.kind = JVal::ARR;
-            ws();
-            if (p < end && *p == ']') { ++p; return true; }
-            while (true) {
-                JVal child;
-                if (!parse(child, depth + 1)) return false;
-                v.arr.push_back(std::move(child));
-                ws();
-                if (p < end && *p == ',') { ++p; continue; }
-                return expect(']');
-            }
-        }
-        if (c == '"') { v.kind = JVal::STR; return parse_string(v.str); }
-        if (c == 't' && end - p >= 4 && !strncmp(p, "true", 4)) { p += 4; v.kind = JVal::BOOL; v.num = 1; return true; }
-        if (c == 'f' && end - p >= 5 && !strncmp(p, "false", 5)) { p += 5; v.kind = JVal::BOOL; return true; }
-        if (c == 'n' && end - p >= 4 && !strncmp(p, "null", 4)) { p += 4; v.kind = JVal::NUL; return true; }
-        if (c == '-' || (c >= '0' && c <= '9')) {
-            const char* q = p;
-            while (q < end && (strchr("+-.eE", *q) || (*q >= '0' && *q <= '9'))) ++q;
-            v.kind = JVal::NUM;
-            v.num = strtod(std::string(p, q).c_str(), nullptr);
-            p = q;
-            return true;
-        }
-        err = "unexpected character";
-        return false;
-    }
-};
 
 float half_to_float(uint16_t h) {
     const uint32_t sign = (uint32_t)(h & 0x8000u) << 16;

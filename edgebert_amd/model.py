@@ -11,7 +11,9 @@ Same entry points and meaning as the Rust API for this path:
   tokenisation (src/lib.rs:588-612)
 * ``Model.encode(texts, normalize)``          <- ``Model::encode`` (src/lib.rs:479-520),
   including its 1000-entry LRU cache keyed ``"{text}||{normalize}"``; needs
-  the HF ``tokenizers`` Tokenizer the reference uses (``tokenizer.json``).
+  a tokenizer (``tokenizer.json``): the library's native WordPiece tokenizer
+  (:class:`~edgebert_amd.tokenizer.Tokenizer`, default) or the HF
+  ``tokenizers`` Tokenizer the reference uses (``tokenizer="hf"``).
 * ``Model.score_pair(query, document)`` / ``score_batch(pairs)`` <-
   ``Model::score_pair`` / ``score_batch`` (src/lib.rs:327-383), for models
   loaded with ``classifier.weight`` / ``classifier.bias``; ``score_ids`` takes
@@ -31,6 +33,7 @@ import numpy as np
 
 from . import _native as N
 from .synth import BertConfig
+from .tokenizer import Tokenizer, c_texts, hf_encode_batch_ids, hf_tokenizer
 
 _DTYPES = {"fp32": N.EBH_DTYPE_F32, "f32": N.EBH_DTYPE_F32, "bf16": N.EBH_DTYPE_BF16}
 
@@ -86,8 +89,12 @@ class Model:
         return cls(h.value, config, dtype, tokenizer)
 
     @classmethod
-    def from_pretrained_path(cls, path: str, dtype: str = "fp32") -> "Model":
-        """``config.json`` + ``model.safetensors`` (+ ``tokenizer.json`` if present)."""
+    def from_pretrained_path(cls, path: str, dtype: str = "fp32", tokenizer: str = "native") -> "Model":
+        """``config.json`` + ``model.safetensors`` (+ ``tokenizer.json`` if present,
+        read by the native tokenizer, or by HF ``tokenizers`` when
+        ``tokenizer="hf"``)."""
+        if tokenizer not in ("native", "hf"):
+            raise ValueError("tokenizer must be 'native' or 'hf'")
         with open(os.path.join(path, "config.json")) as f:
             c = json.load(f)
         config = BertConfig(hidden_size=c["hidden_size"],
@@ -100,21 +107,10 @@ class Model:
                             layer_norm_eps=c.get("layer_norm_eps", 1e-12),
                             hidden_act=c.get("hidden_act", "gelu"),
                             model_type=c.get("model_type", "bert"))
-        tokenizer = None
         tok_path = os.path.join(path, "tokenizer.json")
+        tok = None
         if os.path.exists(tok_path):
-            from tokenizers import Tokenizer  # the tokenizer the reference uses (src/lib.rs:314)
-            tokenizer = Tokenizer.from_file(tok_path)
-            if tokenizer.padding is not None:           # BatchLongest (src/lib.rs:317-319)
-                pad = dict(tokenizer.padding)
-                pad.pop("length", None)
-                tokenizer.enable_padding(**{k: v for k, v in pad.items()
-                                            if k in ("direction", "pad_id", "pad_type_id",
-                                                     "pad_token", "pad_to_multiple_of")})
-            if tokenizer.truncation is not None:        # max_length 512 (src/lib.rs:320-322)
-                tr = dict(tokenizer.truncation)
-                tokenizer.enable_truncation(512, stride=tr.get("stride", 0),
-                                            strategy=tr.get("strategy", "longest_first"))
+            tok = Tokenizer.from_file(tok_path) if tokenizer == "native" else hf_tokenizer(tok_path)
         h = cls._create(config)
         try:
             N.check(N.lib().ebh_load_safetensors(h, os.path.join(path, "model.safetensors").encode()))
@@ -122,7 +118,7 @@ class Model:
         except Exception:
             N.lib().ebh_destroy(h)
             raise
-        return cls(h.value, config, dtype, tokenizer)
+        return cls(h.value, config, dtype, tok)
 
     def close(self):
         if getattr(self, "_h", None) is not None and self._h.value:
@@ -180,14 +176,7 @@ class Model:
                     miss_idx.append(i)
                     miss_txt.append(t)
         if miss_txt:
-            encs = self.tokenizer.encode_batch(miss_txt, add_special_tokens=True)
-            S = max(len(e.ids) for e in encs)
-            ids = np.zeros((len(encs), S), np.uint32)
-            mask = np.zeros((len(encs), S), np.uint32)
-            for r, e in enumerate(encs):
-                ids[r, :len(e.ids)] = e.ids
-                mask[r, :len(e.attention_mask)] = e.attention_mask
-            emb = self.encode_ids(ids, mask, normalize_embeddings)
+            emb = self.encode_texts(miss_txt, normalize_embeddings)
             with self._cache_lock:
                 for r, i in enumerate(miss_idx):
                     vec = emb[r].tolist()
@@ -198,6 +187,24 @@ class Model:
                         self._cache.popitem(last=False)
                     results[i] = list(vec)
         return results
+
+    def encode_texts(self, texts, normalize: bool = True, nthreads: int = 0) -> np.ndarray:
+        """``encode_uncached`` (src/lib.rs:573-619): tokenise and run, no cache.
+        With the native tokenizer one call does both (``ebh_encode_texts``: host
+        threads tokenise into the pinned staging buffers)."""
+        texts = list(texts)
+        out = np.zeros((len(texts), self.config.hidden_size), np.float32)
+        if not texts:
+            return out
+        if isinstance(self.tokenizer, Tokenizer):
+            arr, lens, _keep = c_texts(texts)
+            N.check(N.lib().ebh_encode_texts(self._h, self.tokenizer.handle, arr, _ptr(lens), len(texts),
+                                             1 if normalize else 0, _ptr(out), nthreads))
+            return out
+        if self.tokenizer is None:
+            raise RuntimeError("encode(texts) needs a tokenizer (tokenizer.json)")
+        ids, mask = hf_encode_batch_ids(self.tokenizer, texts)
+        return self.encode_ids(ids.astype(np.uint32), mask.astype(np.uint32), normalize)
 
     def encode_batch(self, batches, normalize_embeddings: bool = True):
         """``encode_batch`` (src/lib.rs:440-451): one ``encode`` per sub-batch."""
@@ -217,22 +224,23 @@ class Model:
         N.check(N.lib().ebh_score(self._h, _ptr(ids), _ptr(mask), B, S, _ptr(out)))
         return out
 
-    def _tokenize_pairs(self, pairs):
+    def _score_texts(self, pairs) -> np.ndarray:
         if self.tokenizer is None:
             raise RuntimeError("score_pair needs a tokenizer (tokenizer.json); use score_ids")
+        if isinstance(self.tokenizer, Tokenizer):
+            qs, ql, _kq = c_texts([q for q, _ in pairs])
+            ds, dl, _kd = c_texts([d for _, d in pairs])
+            out = np.zeros(len(pairs), np.float32)
+            N.check(N.lib().ebh_score_texts(self._h, self.tokenizer.handle, qs, _ptr(ql), ds, _ptr(dl),
+                                            len(pairs), _ptr(out), 0))
+            return out
         texts = [f"{q} [SEP] {d}" for q, d in pairs]      # src/lib.rs:332
-        encs = self.tokenizer.encode_batch(texts, add_special_tokens=True)
-        S = max(len(e.ids) for e in encs)
-        ids = np.zeros((len(encs), S), np.uint32)
-        mask = np.zeros((len(encs), S), np.uint32)
-        for r, e in enumerate(encs):
-            ids[r, :len(e.ids)] = e.ids
-            mask[r, :len(e.attention_mask)] = e.attention_mask
-        return ids, mask
+        ids, mask = hf_encode_batch_ids(self.tokenizer, texts)
+        return self.score_ids(ids.astype(np.uint32), mask.astype(np.uint32))
 
     def score_pair(self, query: str, document: str) -> float:
         """``Model::score_pair`` (src/lib.rs:327-376)."""
-        return float(self.score_ids(*self._tokenize_pairs([(query, document)]))[0])
+        return float(self._score_texts([(query, document)])[0])
 
     def score_batch(self, pairs) -> list:
         """``Model::score_batch`` (src/lib.rs:381-383).  The reference scores the
@@ -242,7 +250,7 @@ class Model:
         pairs = list(pairs)
         if not pairs:
             return []
-        return [float(x) for x in self.score_ids(*self._tokenize_pairs(pairs))]
+        return [float(x) for x in self._score_texts(pairs)]
 
     # ---- device-resident path (bench / integration) ----------------------
     def encode_device(self, ids_ptr: int, mask_ptr: int, B: int, S: int, out_ptr: int,

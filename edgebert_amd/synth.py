@@ -194,3 +194,60 @@ def make_inputs(spec: InputSpec):
     ids[np.arange(B), lengths - 1] = SEP_ID
     mask = (pos < L).astype(np.int32)
     return ids, mask, lengths
+
+
+# ---------------------------------------------------------------------------
+# Synthetic tokenizer.json and texts: every id from 1000 up is a distinct
+# lowercase word, so the texts of a workload tokenise back to its ids exactly
+# (each word is a whole vocabulary entry).
+# ---------------------------------------------------------------------------
+def vocab_word(i: int) -> str:
+    """The word of id ``i`` (>= 1000): ``i`` in base 26 over a..z, prefixed
+    with 'q' (no single letters, no collisions)."""
+    s = ""
+    while True:
+        s = chr(ord("a") + i % 26) + s
+        i //= 26
+        if i == 0:
+            return "q" + s
+
+
+def tokenizer_json(cfg: BertConfig) -> str:
+    """A BERT uncased tokenizer.json over ``cfg.vocab_size`` ids: [PAD] 0,
+    [UNK] 100, [CLS] 101, [SEP] 102, [MASK] 103, [unusedK] up to 999, then
+    :func:`vocab_word` words; BertNormalizer + BertPreTokenizer + WordPiece,
+    [CLS] $A [SEP], truncation and BatchLongest padding."""
+    import json
+    special = {0: "[PAD]", 100: "[UNK]", 101: "[CLS]", 102: "[SEP]", 103: "[MASK]"}
+    vocab = {}
+    for i in range(cfg.vocab_size):
+        vocab[special.get(i, f"[unused{i}]") if i < 1000 else vocab_word(i)] = i
+    added = [{"id": i, "content": t, "single_word": False, "lstrip": False, "rstrip": False,
+              "normalized": False, "special": True} for i, t in sorted(special.items())]
+    tmpl = lambda ids: [{"SpecialToken": {"id": ids[0], "type_id": 0}},  # noqa: E731
+                        {"Sequence": {"id": "A", "type_id": 0}},
+                        {"SpecialToken": {"id": ids[1], "type_id": 0}}]
+    doc = {
+        "version": "1.0",
+        "truncation": {"direction": "Right", "max_length": 128, "strategy": "LongestFirst", "stride": 0},
+        "padding": {"strategy": "BatchLongest", "direction": "Right", "pad_to_multiple_of": None,
+                    "pad_id": 0, "pad_type_id": 0, "pad_token": "[PAD]"},
+        "added_tokens": added,
+        "normalizer": {"type": "BertNormalizer", "clean_text": True, "handle_chinese_chars": True,
+                       "strip_accents": None, "lowercase": True},
+        "pre_tokenizer": {"type": "BertPreTokenizer"},
+        "post_processor": {"type": "TemplateProcessing", "single": tmpl(["[CLS]", "[SEP]"]),
+                           "pair": tmpl(["[CLS]", "[SEP]"]),
+                           "special_tokens": {t: {"id": t, "ids": [i], "tokens": [t]}
+                                              for i, t in ((101, "[CLS]"), (102, "[SEP]"))}},
+        "decoder": None,
+        "model": {"type": "WordPiece", "unk_token": "[UNK]", "continuing_subword_prefix": "##",
+                  "max_input_chars_per_word": 100, "vocab": vocab},
+    }
+    return json.dumps(doc)
+
+
+def make_texts(ids: np.ndarray, lengths) -> list:
+    """The texts whose encodings under :func:`tokenizer_json` are ``ids``
+    ([CLS] words [SEP] rows of a workload)."""
+    return [" ".join(vocab_word(int(t)) for t in ids[b, 1:int(lengths[b]) - 1]) for b in range(ids.shape[0])]

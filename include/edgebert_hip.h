@@ -21,6 +21,7 @@
 #ifndef EDGEBERT_HIP_H
 #define EDGEBERT_HIP_H
 
+#include <stddef.h>
 #include <stdint.h>
 
 #ifndef EBH_API
@@ -137,6 +138,49 @@ EBH_API int ebh_score(ebh_model* m, const uint32_t* ids, const uint32_t* mask, i
  * returns without waiting, as ebh_encode_device. */
 EBH_API int ebh_score_device(ebh_model* m, const int32_t* ids, const int32_t* mask, int32_t B, int32_t S,
                      float* scores, void* stream);
+
+/* ---------------------------------------------------------------------------
+ * Host tokenizer.  Tokenizer::from_file("tokenizer.json") with the reference's
+ * overrides (padding strategy BatchLongest; truncation, when the file has it,
+ * at max_length 512: src/lib.rs:310-322) and encode_batch(texts, true)
+ * (src/lib.rs:577-601), for the BERT tokenizer.json files of the models this
+ * library runs: normalizer BertNormalizer (or none), pre_tokenizer
+ * BertPreTokenizer, model WordPiece, post_processor TemplateProcessing /
+ * BertProcessing (or none), added tokens with normalized = false and
+ * single_word = false.  Other files are rejected with EBH_ERR_SHAPE and a
+ * message naming the unsupported part.  Texts are UTF-8 of lens[i] bytes
+ * (lens == NULL: NUL-terminated; with lengths a text may hold NUL, which
+ * clean_text drops, as Rust strings may); an invalid byte reads as U+FFFD,
+ * which clean_text drops too.  A tokenizer is
+ * immutable after loading and may be shared by any number of threads.
+ * nthreads: host threads to encode on (<= 0: up to 16, one per hardware
+ * thread).
+ * ------------------------------------------------------------------------- */
+typedef struct ebh_tokenizer ebh_tokenizer;
+EBH_API int ebh_tokenizer_load(const char* tokenizer_json_path, ebh_tokenizer** out);
+EBH_API int ebh_tokenizer_from_json(const char* json, size_t len, ebh_tokenizer** out);
+EBH_API void ebh_tokenizer_destroy(ebh_tokenizer* t);
+
+/* encode_batch of n texts, padded to the batch's longest encoding S (rounded
+ * up to the file's pad_to_multiple_of): ids and 0/1 mask written as [n, S]
+ * row-major into buffers of at least n * cap elements; *S_out = S.
+ * EBH_ERR_RANGE if S > cap (nothing written). */
+EBH_API int ebh_tokenize(const ebh_tokenizer* t, const char* const* texts, const int64_t* lens, int32_t n,
+                 int32_t cap, int32_t* ids, int32_t* mask, int32_t* S_out, int32_t nthreads);
+
+/* Model::encode(texts, normalize) without the reference's LRU cache
+ * (encode_uncached, src/lib.rs:573-619): tokenise on the host threads
+ * straight into the model's pinned staging buffers, then the forward; out
+ * [n, hidden_size].  Blocking. */
+EBH_API int ebh_encode_texts(ebh_model* m, const ebh_tokenizer* t, const char* const* texts,
+                     const int64_t* lens, int32_t n, int32_t normalize, float* out, int32_t nthreads);
+
+/* Model::score_batch (src/lib.rs:327-383): pair i is encoded as the single
+ * text "queries[i] [SEP] documents[i]", as score_pair formats it; scores [n]
+ * as ebh_score.  q_lens / d_lens as lens above.  Blocking. */
+EBH_API int ebh_score_texts(ebh_model* m, const ebh_tokenizer* t, const char* const* queries,
+                    const int64_t* q_lens, const char* const* documents, const int64_t* d_lens,
+                    int32_t n, float* scores, int32_t nthreads);
 
 /* Wait for the model's outstanding work; EBH_ERR_RANGE if a device-side id
  * check failed since the previous ebh_synchronize / blocking call. */
