@@ -441,7 +441,7 @@ constexpr int BUFFER_RSRC_WORD3 = 0x00020000;
 // bf16 (round to nearest even) instead of fp32.  LDS offsets below are in
 // 4-byte words, so both element types share the layout and the swizzle.
 template <bool BF16, bool OUT16, int BM, int BN, int BK, int WAVES_M, int WAVES_N, int NSTAGE, int EPI,
-          bool SPREAD = BF16>
+          bool SPREAD = BF16, bool STAGGER = false>
 __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_persistent_kernel(GemmArgs p) {
     constexpr int ES = BF16 ? 2 : 4;              // bytes per element
     constexpr int EPC = 16 / ES;                  // elements per 16-byte chunk
@@ -462,11 +462,16 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_persistent_kernel
     constexpr int LA = A_CH / NT, LW = W_CH / NT, NL = LA + LW;
     constexpr int D = NSTAGE - 1;                 // k-tiles in flight ahead
     constexpr int STAGE = (BM + BN) * RW;         // words per stage: A rows, then W rows
-    static_assert(LN || NW * 32 * WN <= STAGE, "each wave transposes 32 C rows at a time through one stage");
-    static_assert(!LN || 2 * WAVES_N * BM + 2 * NW * 64 <= STAGE, "LayerNorm exchange fits one stage");
     constexpr int C4 = WN / 4;                    // float4 per wave-tile row
-    constexpr int RPP = 64 / C4;                  // wave-tile rows per float4 pass
-    static_assert(LN || (C4 * RPP == 64 && 32 % RPP == 0), "epilogue pass shape");
+    // FLAT: wave tiles too wide for a 32-row transpose per stage, or whose
+    // float4 rows do not tile 64 lanes (e.g. 96 columns): C goes through LDS
+    // 16 rows at a time and the lanes walk the rows' float4 in order.
+    constexpr bool FLAT = !LN && (64 % C4 != 0 || NW * 32 * WN > STAGE);
+    static_assert(LN || FLAT || NW * 32 * WN <= STAGE, "each wave transposes 32 C rows at a time through one stage");
+    static_assert(!FLAT || (NW * 16 * WN <= STAGE && (4 * WN) % 64 == 0), "16-row transpose shape");
+    static_assert(!LN || 2 * WAVES_N * BM + 2 * NW * 64 <= STAGE, "LayerNorm exchange fits one stage");
+    constexpr int RPP = FLAT || LN ? 1 : 64 / C4; // wave-tile rows per float4 pass
+    static_assert(LN || FLAT || (C4 * RPP == 64 && 32 % RPP == 0), "epilogue pass shape");
     constexpr int NPB = 32 / RPP;                 // float4 passes per 32-row block
     constexpr int BIAS_SLOT = 256;                // floats: one wave's 64 x 16-byte bias chunks
 
@@ -700,6 +705,54 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_persistent_kernel
     };
 
     // Epilogue of local tile t: bias (+ GELU), C through LDS stage `cs`, float4 stores.
+    // Bias (+ GELU) of one float4 and its store at (row, gcol).
+    auto put4 = [&](float* Cs, float4 v, const float4& b4, int row, int gcol) __attribute__((always_inline)) {
+        if (HAS_BIAS) { v.x += b4.x; v.y += b4.y; v.z += b4.z; v.w += b4.w; }
+        if constexpr (EPI == EPI_BIAS_GELU) {
+            v.x = gelu_tanh_fast(v.x); v.y = gelu_tanh_fast(v.y);
+            v.z = gelu_tanh_fast(v.z); v.w = gelu_tanh_fast(v.w);
+        }
+        if (gcol < N && row < M) {   // N % 4 == 0: all 4 columns or none
+            if constexpr (OUT16) {
+                uint2 h;
+                h.x = (uint32_t)f32_to_bf16_rne(v.x) | ((uint32_t)f32_to_bf16_rne(v.y) << 16);
+                h.y = (uint32_t)f32_to_bf16_rne(v.z) | ((uint32_t)f32_to_bf16_rne(v.w) << 16);
+                *reinterpret_cast<uint2*>(reinterpret_cast<uint16_t*>(Cs) + (int64_t)row * p.ldc + gcol) = h;
+            } else {
+                *reinterpret_cast<float4*>(Cs + (int64_t)row * p.ldc + gcol) = v;
+            }
+        }
+    };
+    // FLAT epilogue: per 16-row half of each 32-row block (MFMA rows r = 8h ..
+    // 8h+7 hold rows 16h .. 16h+15), C through the wave's 16 x WN slot of LDS
+    // stage `cs`, then float4 q = pass * 64 + lane of those rows in row-major
+    // order.
+    auto epilogue_flat = [&](int t, const float* cs_base) __attribute__((always_inline)) {
+        const int u = wg + t * G, split = u / ntiles, tile = u - split * ntiles;
+        float* const Cs = p.C + (int64_t)split * p.split_stride;
+        const int m0 = (tile / ntiles_n) * BM, n0 = (tile - (tile / ntiles_n) * ntiles_n) * BN;
+        const float* bslot = smem + NSTAGE * STAGE + ((t & 1) * NW + wave) * BIAS_SLOT;
+        float* cw = const_cast<float*>(cs_base) + wave * (16 * WN);
+        constexpr int NPASS = 4 * WN / 64;
+#pragma unroll
+        for (int i = 0; i < FM; ++i)
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+#pragma unroll
+                for (int j = 0; j < FN; ++j)
+#pragma unroll
+                    for (int rr = 0; rr < 8; ++rr)
+                        cw[(8 * (rr >> 2) + 4 * half + (rr & 3)) * WN + j * 32 + l32] = acc[i][j][8 * h + rr];
+#pragma unroll
+                for (int ps = 0; ps < NPASS; ++ps) {
+                    const int q = ps * 64 + lane, lr = q / C4, c = 4 * (q - lr * C4);
+                    const float4 v = *reinterpret_cast<const float4*>(cw + lr * WN + c);
+                    float4 b4 = make_float4(0, 0, 0, 0);
+                    if (HAS_BIAS) b4 = *reinterpret_cast<const float4*>(bslot + c);
+                    put4(Cs, v, b4, m0 + wm * WM + i * 32 + 16 * h + lr, n0 + wn * WN + c);
+                }
+            }
+    };
     auto epilogue_tile = [&](int t, const float* cs_base) {
         const int u = wg + t * G, split = u / ntiles, tile = u - split * ntiles;
         float* const Cs = p.C + (int64_t)split * p.split_stride;
@@ -743,6 +796,7 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_persistent_kernel
 
     auto finish_tile = [&](int t, float* stage) __attribute__((always_inline)) {
         if constexpr (LN) epilogue_ln(t, stage);
+        else if constexpr (FLAT) epilogue_flat(t, stage);
         else epilogue_tile(t, stage);
     };
 
@@ -771,11 +825,15 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_persistent_kernel
                         for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
             }
             const bool refill = nit < total;
-            if (!SPREAD && refill) issue();
+            // STAGGER: the second wave row issues its loads halfway through
+            // the k-tile, so the two waves of each SIMD are not both stalled
+            // at load issue at once.
+            if (!SPREAD && refill && (!STAGGER || wm == 0)) issue();
             const float* st = smem + (it % NSTAGE) * STAGE;
 #pragma unroll
             for (int s = 0; s < KS; ++s) {
                 if (SPREAD && refill) issue_part(s);
+                if (STAGGER && refill && wm != 0 && s == KS / 2) issue();
                 const int ko = 4 * ((2 * s + half) ^ sw);
                 v4f af[FM], wf[FN];
 #pragma unroll
@@ -1058,9 +1116,13 @@ hipError_t launch_gemm_f32(const GemmArgs& a, int epi, hipStream_t s) {
     //  * few tokens (under half a 128 x 128 tile per CU, e.g. the narrow
     //    projections of batch 32 of short sentences): 64 x 64 tiles, two
     //    workgroups per CU, so most CUs have work and their SIMDs a second wave;
-    //  * wide outputs over a short K with many tiles per CU (FFN up at 32k
-    //    tokens): 32-deep k-tiles, two workgroups per CU, so one workgroup's
-    //    GELU epilogue runs beside the other's MFMAs;
+    //  * outputs made of whole 384-column panels with at least one 128 x 384
+    //    tile per CU (QKV and FFN up at 32k tokens): 128 x 384 tiles, 32-deep
+    //    k-tiles, 8 waves of 64 x 96 -- a third fewer load bytes per flop than
+    //    128 x 128 (QKV 297 -> 262 us, FFN up 338 -> 319 us);
+    //  * wide outputs over a short K with many tiles per CU: 32-deep k-tiles,
+    //    two workgroups per CU, so one workgroup's GELU epilogue runs beside
+    //    the other's MFMAs;
     //  * otherwise 128 x 128 tiles, 64-deep k-tiles, 8 waves (two per SIMD).
     //  * split-K (a.splits > 1, bias-free products only): each split is a work
     //    item of its own, written to its own partial output.
@@ -1069,6 +1131,9 @@ hipError_t launch_gemm_f32(const GemmArgs& a, int epi, hipStream_t s) {
     const int64_t tiles128 = (int64_t)((a.M_max + 127) / 128) * ((a.N + 127) / 128);
     if (ok && a.K % (64 * S) == 0 && 2 * tiles128 < (int64_t)cu_count())
         return launch_persistent<64, 64, 64, 2, 2, 2>(a, epi, s, 2);
+    if (ok && S == 1 && a.N % 384 == 0 && a.K % 32 == 0 &&
+        (int64_t)((a.M_max + 127) / 128) * (a.N / 384) >= (int64_t)cu_count())
+        return launch_persistent<128, 384, 32, 2, 4, 2>(a, epi, s, 1);
     if (ok && a.K % 32 == 0 && a.N >= 1536 && a.K < 1024 && tiles128 >= 8 * (int64_t)cu_count() && S == 1)
         return launch_persistent<128, 128, 32, 2, 2, 2>(a, epi, s, 2);
     if (ok && a.K % (64 * S) == 0)
