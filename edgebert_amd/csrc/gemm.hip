@@ -1116,10 +1116,13 @@ hipError_t launch_gemm_f32(const GemmArgs& a, int epi, hipStream_t s) {
     //  * few tokens (under half a 128 x 128 tile per CU, e.g. the narrow
     //    projections of batch 32 of short sentences): 64 x 64 tiles, two
     //    workgroups per CU, so most CUs have work and their SIMDs a second wave;
+    //  * outputs made of whole 256-column panels with at least one 256 x 256
+    //    tile per CU (FFN up at 32k tokens): 256 x 256 tiles, 32-deep k-tiles,
+    //    8 waves of 128 x 64 (FFN up 321 -> 314 us);
     //  * outputs made of whole 384-column panels with at least one 128 x 384
-    //    tile per CU (QKV and FFN up at 32k tokens): 128 x 384 tiles, 32-deep
-    //    k-tiles, 8 waves of 64 x 96 -- a third fewer load bytes per flop than
-    //    128 x 128 (QKV 297 -> 262 us, FFN up 338 -> 319 us);
+    //    tile per CU (QKV at 32k tokens): 128 x 384 tiles, 32-deep k-tiles,
+    //    8 waves of 64 x 96 -- a third fewer load bytes per flop than 128 x 128
+    //    (QKV 297 -> 262 us, FFN up 338 -> 319 us);
     //  * wide outputs over a short K with many tiles per CU: 32-deep k-tiles,
     //    two workgroups per CU, so one workgroup's GELU epilogue runs beside
     //    the other's MFMAs;
@@ -1131,6 +1134,9 @@ hipError_t launch_gemm_f32(const GemmArgs& a, int epi, hipStream_t s) {
     const int64_t tiles128 = (int64_t)((a.M_max + 127) / 128) * ((a.N + 127) / 128);
     if (ok && a.K % (64 * S) == 0 && 2 * tiles128 < (int64_t)cu_count())
         return launch_persistent<64, 64, 64, 2, 2, 2>(a, epi, s, 2);
+    if (ok && S == 1 && a.N % 256 == 0 && a.K % 32 == 0 &&
+        (int64_t)((a.M_max + 255) / 256) * (a.N / 256) >= (int64_t)cu_count())
+        return launch_persistent<256, 256, 32, 2, 4, 2>(a, epi, s, 1);
     if (ok && S == 1 && a.N % 384 == 0 && a.K % 32 == 0 &&
         (int64_t)((a.M_max + 127) / 128) * (a.N / 384) >= (int64_t)cu_count())
         return launch_persistent<128, 384, 32, 2, 4, 2>(a, epi, s, 1);
