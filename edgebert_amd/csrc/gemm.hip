@@ -200,159 +200,6 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_f32_kernel(GemmAr
 }
 
 // ---------------------------------------------------------------------------
-// fp32, direct-to-LDS: the main fp32 kernel when K is a multiple of BK and
-// every row start is 16-byte aligned.
-//
-// Global -> LDS: global_load_lds_dwordx4 (gfx950) moves each lane's 16 bytes
-// straight into LDS, so no VGPRs or ds_write instructions stage the tiles.
-// One such instruction fills 64 consecutive 16-byte LDS chunks per wave, so
-// the tiles are unpadded [rows][BK] and a bank-conflict-free read order comes
-// from an XOR swizzle of the 16-byte chunk within its row instead:
-//   LDS chunk of (row r, k-chunk c) = r * CPR + (c ^ swz(r)),  CPR = BK / 4,
-// and each lane loads the global chunk that belongs at its LDS position.
-// swz spreads any 8 consecutive rows (32 LDS banks) and any 16 consecutive
-// rows (64 banks) over distinct banks for the fragment reads below, where 32
-// lanes read 32 consecutive rows at one k-chunk.
-//
-// Pipeline (two LDS stages, one barrier per k-tile): after the barrier a wave
-// reads all of k-tile kt's fragments into registers, then issues the loads of
-// tile kt+1 into the other stage, then runs the MFMAs of tile kt while those
-// loads land.  The barrier (which waits for the wave's own loads) both
-// publishes tile kt+1 and retires every read of the stage it overwrites.
-// ---------------------------------------------------------------------------
-// One lane's 16 bytes from global memory into LDS (global_load_lds_dwordx4);
-// lds must be the same for every lane of the wave, lane l lands at lds + 16*l bytes.
-__device__ __forceinline__ void load_lds16(const float* g, float* lds) {
-    __builtin_amdgcn_global_load_lds(g, lds, 16, 0, 0);
-}
-
-template <int CPR>
-__device__ __forceinline__ int chunk_swizzle(int r) {
-    static_assert(CPR == 4 || CPR == 8, "BK must be 16 or 32");
-    if constexpr (CPR == 8) return (r & 7) ^ ((r >> 3) & 1);
-    else return ((r >> 1) & 3) ^ ((r >> 3) & 1);
-}
-
-template <int BM, int BN, int BK, int WAVES_M, int WAVES_N, int EPI>
-__global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_f32_dtl_kernel(GemmArgs p) {
-    constexpr int NT = 64 * WAVES_M * WAVES_N;
-    constexpr int WM = BM / WAVES_M, WN = BN / WAVES_N;
-    constexpr int FM = WM / 32, FN = WN / 32;
-    static_assert(FM * 32 == WM && FN * 32 == WN, "wave tile must be whole 32x32 blocks");
-    constexpr int CPR = BK / 4;                   // 16-byte chunks per tile row
-    constexpr int KS = BK / 8;                    // 8-wide k slices per tile
-    constexpr int A_CH = BM * CPR, W_CH = BN * CPR;         // 16-byte chunks per tile
-    constexpr int LA = (A_CH + NT - 1) / NT, LW = (W_CH + NT - 1) / NT;  // loads per thread
-    static_assert(A_CH % 64 == 0 && W_CH % 64 == 0, "a load instruction fills 64 chunks per wave");
-
-    __shared__ __attribute__((aligned(16))) float As[2][BM * BK];
-    __shared__ __attribute__((aligned(16))) float Ws[2][BN * BK];
-
-    const int M = p.M_dev ? *p.M_dev : p.M_max;
-    const int ntiles_n = (p.N + BN - 1) / BN;
-    int mt, nt;
-    tile_coords(ntiles_n, mt, nt);
-    const int m0 = mt * BM, n0 = nt * BN;
-    if (m0 >= M) return;  // uniform over the workgroup
-
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int wm = wave / WAVES_N, wn = wave % WAVES_N;
-    const int l32 = lane & 31, half = lane >> 5;
-    const int N = p.N;
-    const float* __restrict__ A = static_cast<const float*>(p.A);
-    const float* __restrict__ W = static_cast<const float*>(p.W);
-
-    // Global source of each load: LDS chunk P = i*NT + tid holds row P / CPR,
-    // k-chunk (P % CPR) ^ swz(row).  Rows past M / N are clamped (loaded, never stored).
-    const float* a_src[LA];
-    const float* w_src[LW];
-#pragma unroll
-    for (int i = 0; i < LA; ++i) {
-        const int P = i * NT + tid, r = P / CPR, c = (P % CPR) ^ chunk_swizzle<CPR>(r);
-        a_src[i] = A + (int64_t)min(m0 + r, M - 1) * p.lda + c * 4;
-    }
-#pragma unroll
-    for (int i = 0; i < LW; ++i) {
-        const int P = i * NT + tid, r = P / CPR, c = (P % CPR) ^ chunk_swizzle<CPR>(r);
-        w_src[i] = W + (int64_t)min(n0 + r, N - 1) * p.ldw + c * 4;
-    }
-    // Wave-uniform LDS destination of load i: chunks i*NT + wave*64 .. +63.
-    // The last load instruction may cover only part of the tile: whole waves skip it.
-    auto issue = [&](int stage, int k0) {
-#pragma unroll
-        for (int i = 0; i < LA; ++i)
-            if (A_CH % NT == 0 || i * NT + wave * 64 < A_CH)
-                load_lds16(a_src[i] + k0, &As[stage][(i * NT + wave * 64) * 4]);
-#pragma unroll
-        for (int i = 0; i < LW; ++i)
-            if (W_CH % NT == 0 || i * NT + wave * 64 < W_CH)
-                load_lds16(w_src[i] + k0, &Ws[stage][(i * NT + wave * 64) * 4]);
-    };
-
-    // Fragment reads: rows (wave base + 32*i + l32) are 32-aligned, so the swizzle
-    // depends on l32 only.
-    const int sw = chunk_swizzle<CPR>(l32);
-    int koff[KS];
-#pragma unroll
-    for (int s = 0; s < KS; ++s) koff[s] = 4 * ((2 * s + half) ^ sw);
-    const int a_row = (wm * WM + l32) * BK, w_row = (wn * WN + l32) * BK;
-
-    v16f acc[FM][FN];
-#pragma unroll
-    for (int i = 0; i < FM; ++i)
-#pragma unroll
-        for (int j = 0; j < FN; ++j)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
-
-    const int nk = p.K / BK;
-    issue(0, 0);
-    for (int kt = 0; kt < nk; ++kt) {
-        const int cur = kt & 1;
-        __syncthreads();
-        v4f af[KS][FM], wf[KS][FN];
-#pragma unroll
-        for (int s = 0; s < KS; ++s) {
-#pragma unroll
-            for (int i = 0; i < FM; ++i)
-                af[s][i] = *reinterpret_cast<const v4f*>(&As[cur][a_row + i * 32 * BK + koff[s]]);
-#pragma unroll
-            for (int j = 0; j < FN; ++j)
-                wf[s][j] = *reinterpret_cast<const v4f*>(&Ws[cur][w_row + j * 32 * BK + koff[s]]);
-        }
-        if (kt + 1 < nk) issue(cur ^ 1, (kt + 1) * BK);
-#pragma unroll
-        for (int s = 0; s < KS; ++s)
-#pragma unroll
-            for (int q = 0; q < 4; ++q)
-#pragma unroll
-                for (int i = 0; i < FM; ++i)
-#pragma unroll
-                    for (int j = 0; j < FN; ++j)
-                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(af[s][i][q], wf[s][j][q],
-                                                                         acc[i][j], 0, 0, 0);
-    }
-
-#pragma unroll
-    for (int j = 0; j < FN; ++j) {
-        const int col = n0 + wn * WN + j * 32 + l32;
-        if (col >= N) continue;
-        const float bcol = p.bias[col];
-#pragma unroll
-        for (int i = 0; i < FM; ++i) {
-            const int rbase = m0 + wm * WM + i * 32 + 4 * half;
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const int row = rbase + 8 * (r >> 2) + (r & 3);
-                if (row < M)
-                    p.C[(int64_t)row * p.ldc + col] =
-                        epilogue<EPI>(acc[i][j][r], bcol, p.R, p.ldr, row, col);
-            }
-        }
-    }
-}
-
-// ---------------------------------------------------------------------------
 // fp32, persistent: one workgroup per CU walks a strided list of BM x BN C
 // tiles through one flattened (tile, k-tile) pipeline with NSTAGE LDS stages,
 // so the loads of the next NSTAGE-1 k-tiles (across tile boundaries) are in
@@ -375,47 +222,6 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_f32_dtl_kernel(Ge
 // row-contiguous float4.  Its stores are then older than every load still to
 // be waited for, so no later wait depends on them finishing early.
 // ---------------------------------------------------------------------------
-__device__ __forceinline__ void load_lds16_async(const void* g, const float* lds) {
-    const uint32_t base = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)lds);
-    uint32_t saved;
-    asm volatile(
-        "s_mov_b32 %0, m0\n\t"
-        "s_mov_b32 m0, %2\n\t"
-        "s_nop 0\n\t"
-        "global_load_lds_dwordx4 %1, off\n\t"
-        "s_mov_b32 m0, %0"
-        : "=&s"(saved)
-        : "v"(g), "s"(base)
-        : "memory");
-}
-
-// At most n vector-memory operations of this wave outstanding (n is
-// wave-uniform; s_waitcnt takes an immediate, so switch over the small range
-// the pipelines use; larger n waits for everything, which is always safe).
-__device__ __forceinline__ void wait_vmcnt(int n) {
-    switch (n) {
-#define EBH_VMCNT(k) \
-    case k: asm volatile("s_waitcnt vmcnt(" #k ")" ::: "memory"); break;
-        EBH_VMCNT(1) EBH_VMCNT(2) EBH_VMCNT(3) EBH_VMCNT(4) EBH_VMCNT(5) EBH_VMCNT(6)
-        EBH_VMCNT(7) EBH_VMCNT(8) EBH_VMCNT(9) EBH_VMCNT(10) EBH_VMCNT(11) EBH_VMCNT(12)
-        EBH_VMCNT(13) EBH_VMCNT(14) EBH_VMCNT(15) EBH_VMCNT(16) EBH_VMCNT(17) EBH_VMCNT(18)
-        EBH_VMCNT(19) EBH_VMCNT(20) EBH_VMCNT(21) EBH_VMCNT(22) EBH_VMCNT(23) EBH_VMCNT(24)
-#undef EBH_VMCNT
-        default: asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); break;
-    }
-}
-
-// This wave's LDS reads have returned; then the workgroup barrier.
-__device__ __forceinline__ void lds_barrier() {
-    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-}
-
-template <int CPR>
-__device__ __forceinline__ int chunk_swizzle16(int r) {
-    if constexpr (CPR == 16) return r & 15;
-    else return chunk_swizzle<CPR>(r);
-}
-
 // tanh-form GELU of the reference (constants of src/lib.rs:151-152),
 // 0.5 x (1 + tanh(u)) with u = sqrt(2/pi) (x + 0.044715 x^3), evaluated as
 // x * sigmoid(2u) = x / (1 + e^(-2u)) on the hardware exp2 and reciprocal:
@@ -1041,33 +847,9 @@ static hipError_t launch_tile(const GemmArgs& a, int epi, hipStream_t s) {
     return hipGetLastError();
 }
 
-template <int BM, int BN, int BK, int WAVES_M, int WAVES_N>
-static hipError_t launch_dtl(const GemmArgs& a, int epi, hipStream_t s) {
-    const int mt = (a.M_max + BM - 1) / BM, nt = (a.N + BN - 1) / BN;
-    const dim3 grid(mt * nt), block(64 * WAVES_M * WAVES_N);
-    if (mt == 0 || nt == 0) return hipSuccess;
-    switch (epi) {
-        case EPI_BIAS:
-            hipLaunchKernelGGL((gemm_f32_dtl_kernel<BM, BN, BK, WAVES_M, WAVES_N, EPI_BIAS>), grid, block, 0, s, a);
-            break;
-        case EPI_BIAS_GELU:
-            hipLaunchKernelGGL((gemm_f32_dtl_kernel<BM, BN, BK, WAVES_M, WAVES_N, EPI_BIAS_GELU>), grid, block, 0, s, a);
-            break;
-        case EPI_BIAS_RESID:
-            hipLaunchKernelGGL((gemm_f32_dtl_kernel<BM, BN, BK, WAVES_M, WAVES_N, EPI_BIAS_RESID>), grid, block, 0, s, a);
-            break;
-        case EPI_NONE:
-            hipLaunchKernelGGL((gemm_f32_dtl_kernel<BM, BN, BK, WAVES_M, WAVES_N, EPI_NONE>), grid, block, 0, s, a);
-            break;
-        default:
-            return hipErrorInvalidValue;
-    }
-    return hipGetLastError();
-}
-
 // Persistent launch: min(tiles, CUs) workgroups (one per CU: the two LDS
 // stages take 128 KB at BK = 64).
-static int cu_count() {
+int device_cu_count() {
     static int n = 0;
     if (n == 0) {
         int dev = 0, v = 0;
@@ -1079,6 +861,8 @@ static int cu_count() {
     }
     return n;
 }
+
+static int cu_count() { return device_cu_count(); }
 
 template <int BM, int BN, int BK, int WAVES_M, int WAVES_N, int NSTAGE, bool BF16 = false, bool OUT16 = false>
 static hipError_t launch_persistent(const GemmArgs& a, int epi, hipStream_t s, int wg_per_cu = 1) {
@@ -1119,10 +903,11 @@ hipError_t launch_gemm_f32(const GemmArgs& a, int epi, hipStream_t s) {
     //  * outputs made of whole 256-column panels with at least one 256 x 256
     //    tile per CU (FFN up at 32k tokens): 256 x 256 tiles, 32-deep k-tiles,
     //    8 waves of 128 x 64 (FFN up 321 -> 314 us);
-    //  * outputs made of whole 384-column panels with at least one 128 x 384
-    //    tile per CU (QKV at 32k tokens): 128 x 384 tiles, 32-deep k-tiles,
-    //    8 waves of 64 x 96 -- a third fewer load bytes per flop than 128 x 128
-    //    (QKV 297 -> 262 us, FFN up 338 -> 319 us);
+    //  * otherwise outputs made of whole 192-column panels with at least one
+    //    256 x 192 tile per CU (QKV at 32k tokens): 256 x 192 tiles, 32-deep
+    //    k-tiles, 8 waves of 64 x 96.  Both wide tiles load far fewer bytes per
+    //    flop than 128 x 128 (QKV 297 -> 262 us at 128 x 384, 252 -> 243 us
+    //    at 256 x 192; FFN up 338 -> 319 us at 128 x 384);
     //  * wide outputs over a short K with many tiles per CU: 32-deep k-tiles,
     //    two workgroups per CU, so one workgroup's GELU epilogue runs beside
     //    the other's MFMAs;
@@ -1137,9 +922,9 @@ hipError_t launch_gemm_f32(const GemmArgs& a, int epi, hipStream_t s) {
     if (ok && S == 1 && a.N % 256 == 0 && a.K % 32 == 0 &&
         (int64_t)((a.M_max + 255) / 256) * (a.N / 256) >= (int64_t)cu_count())
         return launch_persistent<256, 256, 32, 2, 4, 2>(a, epi, s, 1);
-    if (ok && S == 1 && a.N % 384 == 0 && a.K % 32 == 0 &&
-        (int64_t)((a.M_max + 127) / 128) * (a.N / 384) >= (int64_t)cu_count())
-        return launch_persistent<128, 384, 32, 2, 4, 2>(a, epi, s, 1);
+    if (ok && S == 1 && a.N % 192 == 0 && a.K % 32 == 0 &&
+        (int64_t)((a.M_max + 255) / 256) * (a.N / 192) >= (int64_t)cu_count())
+        return launch_persistent<256, 192, 32, 4, 2, 2>(a, epi, s, 1);
     if (ok && a.K % 32 == 0 && a.N >= 1536 && a.K < 1024 && tiles128 >= 8 * (int64_t)cu_count() && S == 1)
         return launch_persistent<128, 128, 32, 2, 2, 2>(a, epi, s, 2);
     if (ok && a.K % (64 * S) == 0)

@@ -31,6 +31,9 @@ struct GemmArgs {
     float ln_eps;
 };
 
+// Compute units of the current device (queried once).
+int device_cu_count();
+
 // Split count launch_gemm_f32 takes best for a bias-free product of this shape
 // (1 unless there are too few tiles to fill the chip); the caller provides
 // `splits` partial outputs.
@@ -135,6 +138,60 @@ __device__ __forceinline__ float gelu_tanh(float val) {
     float val_cubed = val * val * val;
     float inner = SQRT_2_OVER_PI * (val + GELU_COEFF * val_cubed);
     return val * 0.5f * (1.0f + tanhf(inner));
+}
+
+// One lane's 16 bytes from global memory straight into LDS
+// (global_load_lds_dwordx4): lane l of the wave lands at lds + 16 l bytes, so
+// `lds` must be the same for every lane.  Issued from inline asm so that the
+// compiler's wait-count tracking does not see it (it would otherwise make
+// every LDS read wait for every outstanding load); callers wait explicitly
+// with wait_vmcnt.  M0 (the instruction's LDS base) is saved and restored.
+__device__ __forceinline__ void load_lds16_async(const void* g, const float* lds) {
+    const uint32_t base = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)lds);
+    uint32_t saved;
+    asm volatile(
+        "s_mov_b32 %0, m0\n\t"
+        "s_mov_b32 m0, %2\n\t"
+        "s_nop 0\n\t"
+        "global_load_lds_dwordx4 %1, off\n\t"
+        "s_mov_b32 m0, %0"
+        : "=&s"(saved)
+        : "v"(g), "s"(base)
+        : "memory");
+}
+
+// At most n vector-memory operations of this wave outstanding (n is
+// wave-uniform; s_waitcnt takes an immediate, so switch over the small range
+// the pipelines use; larger n waits for everything, which is always safe).
+// Vector memory operations complete in issue order.
+__device__ __forceinline__ void wait_vmcnt(int n) {
+    switch (n) {
+#define EBH_VMCNT(k) \
+    case k: asm volatile("s_waitcnt vmcnt(" #k ")" ::: "memory"); break;
+        EBH_VMCNT(1) EBH_VMCNT(2) EBH_VMCNT(3) EBH_VMCNT(4) EBH_VMCNT(5) EBH_VMCNT(6)
+        EBH_VMCNT(7) EBH_VMCNT(8) EBH_VMCNT(9) EBH_VMCNT(10) EBH_VMCNT(11) EBH_VMCNT(12)
+        EBH_VMCNT(13) EBH_VMCNT(14) EBH_VMCNT(15) EBH_VMCNT(16) EBH_VMCNT(17) EBH_VMCNT(18)
+        EBH_VMCNT(19) EBH_VMCNT(20) EBH_VMCNT(21) EBH_VMCNT(22) EBH_VMCNT(23) EBH_VMCNT(24)
+#undef EBH_VMCNT
+        default: asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); break;
+    }
+}
+
+// This wave's LDS reads have returned; then the workgroup barrier.
+__device__ __forceinline__ void lds_barrier() {
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
+// XOR swizzle of the 16-byte chunk index within an LDS row of CPR chunks
+// (tiles stored unpadded, [rows][CPR chunks]): chunk c of row r lives at
+// c ^ chunk_swizzle16<CPR>(r).  32 lanes reading one chunk of 32 consecutive
+// rows then spread over all banks (checked for 32 and 64 banks).
+template <int CPR>
+__device__ __forceinline__ int chunk_swizzle16(int r) {
+    static_assert(CPR == 4 || CPR == 8 || CPR == 16, "4, 8 or 16 chunks per row");
+    if constexpr (CPR == 16) return r & 15;
+    else if constexpr (CPR == 8) return (r & 7) ^ ((r >> 3) & 1);
+    else return ((r >> 1) & 3) ^ ((r >> 3) & 1);
 }
 
 __device__ __forceinline__ uint16_t f32_to_bf16_rne(float f) {

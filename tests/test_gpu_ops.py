@@ -83,9 +83,9 @@ def test_gemm_f32(env, M, N, K, epi):
     (4100, 1152, 384, 0),      # 128 x 128 tiles, 8 waves (row tail of 4)
     (8192, 384, 1536, 3),      # 8 waves, long K, no bias
     (33000, 1536, 384, 1),     # 256 x 256 tiles (GELU), ragged last row block: FFN up
-    (32768, 1152, 384, 0),     # 128 x 384 tiles (bias): QKV at 256 x 128 tokens
-    (20000, 1152, 384, 1),     # 128 x 384 tiles (GELU), ragged last row block
-    (20000, 768, 256, 3),      # 128 x 384 tiles, no bias, 8 k-tiles
+    (32768, 1152, 384, 0),     # 256 x 192 tiles (bias): QKV at 256 x 128 tokens
+    (20000, 1152, 384, 1),     # 256 x 192 tiles (GELU), ragged last row block
+    (40000, 576, 256, 3),      # 256 x 192 tiles, no bias, 8 k-tiles
     (40000, 512, 160, 3),      # 256 x 256 tiles, no bias, 5 k-tiles
     (9000, 1024, 384, 1),      # 128 x 128 tiles beside the 128 x 384 case (N not whole panels)
     (500, 256, 96, 0),         # K % 64 != 0: 32-deep k-tiles
