@@ -247,7 +247,7 @@ constexpr int BUFFER_RSRC_WORD3 = 0x00020000;
 // bf16 (round to nearest even) instead of fp32.  LDS offsets below are in
 // 4-byte words, so both element types share the layout and the swizzle.
 template <bool BF16, bool OUT16, int BM, int BN, int BK, int WAVES_M, int WAVES_N, int NSTAGE, int EPI,
-          bool SPREAD = BF16, bool STAGGER = false>
+          bool SPREAD = BF16>
 __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_persistent_kernel(GemmArgs p) {
     constexpr int ES = BF16 ? 2 : 4;              // bytes per element
     constexpr int EPC = 16 / ES;                  // elements per 16-byte chunk
@@ -631,15 +631,11 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_persistent_kernel
                         for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
             }
             const bool refill = nit < total;
-            // STAGGER: the second wave row issues its loads halfway through
-            // the k-tile, so the two waves of each SIMD are not both stalled
-            // at load issue at once.
-            if (!SPREAD && refill && (!STAGGER || wm == 0)) issue();
+            if (!SPREAD && refill) issue();
             const float* st = smem + (it % NSTAGE) * STAGE;
 #pragma unroll
             for (int s = 0; s < KS; ++s) {
                 if (SPREAD && refill) issue_part(s);
-                if (STAGGER && refill && wm != 0 && s == KS / 2) issue();
                 const int ko = 4 * ((2 * s + half) ^ sw);
                 v4f af[FM], wf[FN];
 #pragma unroll
