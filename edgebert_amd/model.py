@@ -206,9 +206,28 @@ class Model:
         ids, mask = hf_encode_batch_ids(self.tokenizer, texts)
         return self.encode_ids(ids.astype(np.uint32), mask.astype(np.uint32), normalize)
 
-    def encode_batch(self, batches, normalize_embeddings: bool = True):
-        """``encode_batch`` (src/lib.rs:440-451): one ``encode`` per sub-batch."""
-        return [self.encode(b, normalize_embeddings) for b in batches]
+    def encode_batch(self, batches, normalize_embeddings: bool = True, workers: int = 2):
+        """``encode_batch`` (src/lib.rs:438-450): one ``encode`` per sub-batch, the
+        sub-batches run concurrently as the reference's rayon ``par_iter`` runs
+        them.  The model serialises its forwards, but a sub-batch's
+        tokenisation (host threads, outside the model's lock) overlaps the
+        previous sub-batch's forward on the GPU."""
+        batches = [list(b) for b in batches]
+        if workers <= 1 or len(batches) <= 1:
+            return [self.encode(b, normalize_embeddings) for b in batches]
+        from concurrent.futures import ThreadPoolExecutor
+        with ThreadPoolExecutor(max_workers=min(workers, len(batches))) as pool:
+            return list(pool.map(lambda b: self.encode(b, normalize_embeddings), batches))
+
+    def encode_texts_many(self, batches, normalize: bool = True, workers: int = 2) -> list:
+        """``encode_texts`` of several sub-batches (no cache), run as
+        ``encode_batch`` runs them: ``[n_i, H]`` arrays in order."""
+        batches = [list(b) for b in batches]
+        if workers <= 1 or len(batches) <= 1:
+            return [self.encode_texts(b, normalize) for b in batches]
+        from concurrent.futures import ThreadPoolExecutor
+        with ThreadPoolExecutor(max_workers=min(workers, len(batches))) as pool:
+            return list(pool.map(lambda b: self.encode_texts(b, normalize), batches))
 
     # ---- cross-encoder (score_pair / score_batch) ------------------------
     def score_ids(self, ids, mask) -> np.ndarray:

@@ -65,3 +65,22 @@ def test_score_texts_matches_hf_tokenised_pairs(eb, weights_for, tmp_path):
     want = m.score_ids(ids.astype(np.uint32), mask.astype(np.uint32))
     assert np.array_equal(got, want)
     assert m.score_pair(qs[3], ds[3]) == pytest.approx(float(got[3]), abs=2e-6)
+
+
+def test_encode_batch_runs_sub_batches_concurrently_with_the_same_results(eb, weights_for):
+    """encode_batch (src/lib.rs:438-450) over sub-batches on two host threads:
+    every vector equal to its sub-batch encoded alone."""
+    from edgebert_amd import synth
+    spec = eb.CONFIGS["c2"]
+    ids, mask, lengths = eb.make_inputs(spec)
+    tok = eb.Tokenizer.from_str(synth.tokenizer_json(spec.model))
+    texts = synth.make_texts(ids, lengths)
+    subs = [texts[0:10], texts[10:11], texts[11:32]]
+    m = eb.Model.from_weights(weights_for(spec.model), spec.model, "fp32", tokenizer=tok)
+    alone = [m.encode_texts(b, True) for b in subs]
+    many = m.encode_texts_many(subs, True, workers=2)
+    for a, b in zip(alone, many):
+        assert np.array_equal(a, b)
+    lists = m.encode_batch(subs, True, workers=2)
+    for a, b in zip(alone, lists):
+        assert np.array_equal(a, np.array(b, np.float32))
