@@ -100,6 +100,27 @@ def test_c3_subsample_and_properties(eb, oracle_mod, weights_for):
     assert np.array_equal(got_d[0::2], got_d[1::2])
 
 
+def test_large_ragged_batch_takes_the_fused_paths(eb, oracle_mod, weights_for):
+    """512 sequences of 64..128 tokens: the grid is sized for 512 x 128 rows but
+    only the packed tokens exist, so the wide-tile GEMMs and the fused
+    GEMM + LayerNorm run with fewer real rows than their tiles cover (ragged
+    last row block, descriptors ending at the packed count).  24 sequences
+    against the oracle, all rows finite and unit-norm."""
+    from edgebert_amd.synth import InputSpec, MINILM_L6, make_inputs
+    spec = InputSpec("ragged512", MINILM_L6, 512, 128, 64, 128, 11)
+    w = weights_for(spec.model)
+    ids, mask, lengths = make_inputs(spec)
+    assert 512 * 64 < int(mask.sum()) < 512 * 128
+    m = gpu_model(eb, spec.model, w)
+    got = m.encode_ids(ids, mask, normalize=True)
+    assert np.isfinite(got).all()
+    np.testing.assert_allclose(np.linalg.norm(got.astype(np.float64), axis=1), 1.0, atol=1e-5)
+    sel = np.arange(0, spec.batch, spec.batch // 24)[:24]
+    want = oracle_mod.OracleModel(spec.model, w).encode_unpadded(ids[sel], mask[sel], normalize=True)
+    err, cos = _report("ragged 512 subsample", got[sel], want)
+    assert err <= FP32_MAX_ABS and cos >= FP32_MIN_COS
+
+
 def test_bf16_bert_base(eb, oracle_mod, weights_for):
     """c5 shape (BERT-base, head_dim 64) with bf16 GEMMs on a 24-sequence sample."""
     spec = eb.CONFIGS["c5"]
