@@ -161,8 +161,8 @@ __device__ __forceinline__ void load_lds16_async(const void* g, const float* lds
 }
 
 // At most n vector-memory operations of this wave outstanding (n is
-// wave-uniform; s_waitcnt takes an immediate, so switch over the small range
-// the pipelines use; larger n waits for everything, which is always safe).
+// wave-uniform; s_waitcnt takes an immediate, so switch over the counter's
+// range, 0..63; larger n waits for everything, which is always safe).
 // Vector memory operations complete in issue order.
 __device__ __forceinline__ void wait_vmcnt(int n) {
     switch (n) {
@@ -172,6 +172,13 @@ __device__ __forceinline__ void wait_vmcnt(int n) {
         EBH_VMCNT(7) EBH_VMCNT(8) EBH_VMCNT(9) EBH_VMCNT(10) EBH_VMCNT(11) EBH_VMCNT(12)
         EBH_VMCNT(13) EBH_VMCNT(14) EBH_VMCNT(15) EBH_VMCNT(16) EBH_VMCNT(17) EBH_VMCNT(18)
         EBH_VMCNT(19) EBH_VMCNT(20) EBH_VMCNT(21) EBH_VMCNT(22) EBH_VMCNT(23) EBH_VMCNT(24)
+        EBH_VMCNT(25) EBH_VMCNT(26) EBH_VMCNT(27) EBH_VMCNT(28) EBH_VMCNT(29) EBH_VMCNT(30)
+        EBH_VMCNT(31) EBH_VMCNT(32) EBH_VMCNT(33) EBH_VMCNT(34) EBH_VMCNT(35) EBH_VMCNT(36)
+        EBH_VMCNT(37) EBH_VMCNT(38) EBH_VMCNT(39) EBH_VMCNT(40) EBH_VMCNT(41) EBH_VMCNT(42)
+        EBH_VMCNT(43) EBH_VMCNT(44) EBH_VMCNT(45) EBH_VMCNT(46) EBH_VMCNT(47) EBH_VMCNT(48)
+        EBH_VMCNT(49) EBH_VMCNT(50) EBH_VMCNT(51) EBH_VMCNT(52) EBH_VMCNT(53) EBH_VMCNT(54)
+        EBH_VMCNT(55) EBH_VMCNT(56) EBH_VMCNT(57) EBH_VMCNT(58) EBH_VMCNT(59) EBH_VMCNT(60)
+        EBH_VMCNT(61) EBH_VMCNT(62) EBH_VMCNT(63)
 #undef EBH_VMCNT
         default: asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); break;
     }

@@ -121,6 +121,20 @@ def test_large_ragged_batch_takes_the_fused_paths(eb, oracle_mod, weights_for):
     assert err <= FP32_MAX_ABS and cos >= FP32_MIN_COS
 
 
+def test_bert_base_fp32_few_tokens_split_k(eb, oracle_mod, weights_for):
+    """BERT-base in fp32 with 3 short sentences: the bias-free projections are
+    split over K (6 splits at K = 768, 8 at K = 3072) into partial products
+    that the LayerNorm sums in order."""
+    from edgebert_amd.synth import InputSpec, BERT_BASE, make_inputs
+    spec = InputSpec("bert_few", BERT_BASE, 3, 24, 5, 24, 12)
+    w = weights_for(spec.model)
+    ids, mask, _ = make_inputs(spec)
+    got = gpu_model(eb, spec.model, w).encode_ids(ids, mask, normalize=True)
+    want = oracle_mod.OracleModel(spec.model, w).encode_unpadded(ids, mask, normalize=True)
+    err, cos = _report("BERT-base fp32 few tokens", got, want)
+    assert err <= FP32_MAX_ABS and cos >= FP32_MIN_COS
+
+
 def test_bf16_bert_base(eb, oracle_mod, weights_for):
     """c5 shape (BERT-base, head_dim 64) with bf16 GEMMs on a 24-sequence sample."""
     spec = eb.CONFIGS["c5"]
