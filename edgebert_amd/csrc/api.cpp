@@ -395,7 +395,7 @@ int enqueue_forward(ebh_model* m, const int* d_ids, const int* d_mask, int B, in
         if (bf16)
             HIP_TRY(ebh::launch_attention_bf16(qkv16, w.cu, B, S, H, nh, hd, scale, ctx16, s));
         else
-            HIP_TRY(ebh::launch_attention(w.QKV, w.cu, B, S, H, nh, hd, scale, w.CTX, false, s));
+            HIP_TRY(ebh::launch_attention(w.QKV, w.cu, B, S, H, nh, hd, scale, w.CTX, s));
         prof_end(m, s, pp, on);
         if (fuse_out) {
             if ((rc = gemm_ln(EBH_PROF_GEMM_OUT, w.CTX, L.wo, L.bo, L.ln1_g, L.ln1_b, H))) return rc;
@@ -995,7 +995,7 @@ int ebh_op_attention(const float* qkv, const int32_t* cu_seqlens, int32_t B, int
         return fail(EBH_ERR_INVALID_ARG, "qkv and ctx must be 16-byte aligned");
     const float scale = 1.0f / sqrtf((float)hd);
     HIP_TRY(ebh::launch_attention(qkv, cu_seqlens, B, max_len, hidden, num_heads, hd, scale, ctx,
-                                  false, static_cast<hipStream_t>(stream)));
+                                  static_cast<hipStream_t>(stream)));
     return EBH_OK;
 }
 

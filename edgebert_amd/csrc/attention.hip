@@ -30,10 +30,10 @@ namespace ebh {
 typedef float v16f __attribute__((ext_vector_type(16)));
 typedef float v4f __attribute__((ext_vector_type(4)));
 
-template <int HD, bool OUT16>
+template <int HD>
 __global__ __launch_bounds__(256) void attention_kernel(const float* __restrict__ qkv,
                                                         const int* __restrict__ cu_seqlens,
-                                                        void* __restrict__ ctx_out, int H,
+                                                        float* __restrict__ ctx_out, int H,
                                                         float scale) {
     constexpr int KC = 128;        // keys per LDS chunk
     constexpr int KS = HD + 4;     // K row stride (floats): conflict-free 16-B reads
@@ -165,15 +165,7 @@ __global__ __launch_bounds__(256) void attention_kernel(const float* __restrict_
             for (int g = 0; g < 4; ++g) {
                 const float c0 = o[j][4 * g] * inv, c1 = o[j][4 * g + 1] * inv;
                 const float c2 = o[j][4 * g + 2] * inv, c3 = o[j][4 * g + 3] * inv;
-                const int64_t d = at + j * 32 + 8 * g;
-                if constexpr (OUT16) {
-                    uint2 h;
-                    h.x = (uint32_t)f32_to_bf16_rne(c0) | ((uint32_t)f32_to_bf16_rne(c1) << 16);
-                    h.y = (uint32_t)f32_to_bf16_rne(c2) | ((uint32_t)f32_to_bf16_rne(c3) << 16);
-                    *reinterpret_cast<uint2*>(static_cast<uint16_t*>(ctx_out) + d) = h;
-                } else {
-                    *reinterpret_cast<float4*>(static_cast<float*>(ctx_out) + d) = make_float4(c0, c1, c2, c3);
-                }
+                *reinterpret_cast<float4*>(ctx_out + at + j * 32 + 8 * g) = make_float4(c0, c1, c2, c3);
             }
     }
 }
@@ -382,18 +374,13 @@ hipError_t launch_attention_bf16(const uint16_t* qkv, const int* cu_seqlens, int
 }
 
 hipError_t launch_attention(const float* qkv, const int* cu_seqlens, int B, int max_len, int H,
-                            int nh, int head_dim, float scale, void* ctx, bool ctx_bf16,
-                            hipStream_t s) {
+                            int nh, int head_dim, float scale, float* ctx, hipStream_t s) {
     if (B <= 0 || max_len <= 0) return hipSuccess;
     const dim3 grid(nh, (max_len + 127) / 128, B), block(256);
-    if (head_dim == 32 && !ctx_bf16)
-        hipLaunchKernelGGL((attention_kernel<32, false>), grid, block, 0, s, qkv, cu_seqlens, ctx, H, scale);
-    else if (head_dim == 32)
-        hipLaunchKernelGGL((attention_kernel<32, true>), grid, block, 0, s, qkv, cu_seqlens, ctx, H, scale);
-    else if (head_dim == 64 && !ctx_bf16)
-        hipLaunchKernelGGL((attention_kernel<64, false>), grid, block, 0, s, qkv, cu_seqlens, ctx, H, scale);
+    if (head_dim == 32)
+        hipLaunchKernelGGL(attention_kernel<32>, grid, block, 0, s, qkv, cu_seqlens, ctx, H, scale);
     else if (head_dim == 64)
-        hipLaunchKernelGGL((attention_kernel<64, true>), grid, block, 0, s, qkv, cu_seqlens, ctx, H, scale);
+        hipLaunchKernelGGL(attention_kernel<64>, grid, block, 0, s, qkv, cu_seqlens, ctx, H, scale);
     else
         return hipErrorInvalidValue;
     return hipGetLastError();

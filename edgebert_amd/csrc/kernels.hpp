@@ -44,11 +44,9 @@ hipError_t launch_gemm_f32(const GemmArgs& a, int epi, hipStream_t s);
 hipError_t launch_gemm_bf16(const GemmArgs& a, int epi, hipStream_t s);
 
 // Masked multi-head attention over packed sequences: qkv [T, 3H] rows
-// (q | k | v), cu_seqlens [B+1]; ctx [T, H] fp32, or bf16 bits when ctx_bf16.
-// head_dim 32 or 64.
+// (q | k | v), cu_seqlens [B+1]; ctx [T, H].  head_dim 32 or 64.
 hipError_t launch_attention(const float* qkv, const int* cu_seqlens, int B, int max_len,
-                            int H, int nh, int head_dim, float scale, void* ctx, bool ctx_bf16,
-                            hipStream_t s);
+                            int H, int nh, int head_dim, float scale, float* ctx, hipStream_t s);
 
 // Attention with bf16 q / k / v (qkv [T, 3H] bf16 bits) and bf16 context;
 // scores, softmax and accumulation in fp32.  head_dim 32 or 64.
