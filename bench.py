@@ -11,7 +11,8 @@ stream its launches go to; its ``traffic`` (HBM bytes per launch) is read from
 the committed rocprofv3 counter summary for the same workload and kernel, when
 there is one.  ``cpu_baseline`` times the repo's C restatement of the
 reference CPU path (``oracle/``) on a bounded sample of the same workload on
-this host.  ``host_api`` is the rate of the blocking host-buffer entry point
+this host, with its built-in sgemm (the reference's default build) and with
+OpenBLAS (its ``openblas`` feature).  ``host_api`` is the rate of the blocking host-buffer entry point
 (``ebh_encode``: ids / mask copied in over PCIe, vectors copied back); it is
 reported beside ``value``, never as it.  ``encode_texts`` is the rate from
 texts (``Model::encode`` without its cache): the native tokenizer on host
@@ -95,25 +96,48 @@ def measured_traffic(config: str, kernel: str, dtype: str):
 
 def cpu_baseline(spec, weights, ids, mask, budget_s: float):
     """Oracle (C port of the reference CPU path) on chunks of 16 sequences of
-    the same workload until ``budget_s`` has elapsed (after one warm-up chunk)."""
+    the same workload, in the reference's two builds: the default features
+    (matrixmultiply sgemm, restated in oracle.c) and ``--features openblas``
+    (every product on OpenBLAS's cblas_sgemm, here the OpenBLAS numpy links).
+    Each runs for half of ``budget_s`` after one warm-up chunk; ``value`` is
+    the faster of the two."""
     import oracle
     om = oracle.OracleModel(spec.model, weights)
     chunk = 16
-    om.encode(ids[:chunk], mask[:chunk])           # warm-up
-    done, t0, i = 0, time.perf_counter(), 0
-    while True:
-        lo = (i * chunk) % spec.batch
-        om.encode(ids[lo:lo + chunk], mask[lo:lo + chunk])
-        done += chunk
-        i += 1
-        el = time.perf_counter() - t0
-        if el >= budget_s:
-            break
-    return {"value": round(done / el, 3), "unit": "sentences/s",
-            "cores": oracle.get_num_threads(), "kind": "port",
-            "sample": f"{done} sequences of the {spec.name} workload (seq {spec.seq_len}) in "
-                      f"chunks of {chunk}, {el:.1f} s, oracle/liboracle.so on "
-                      f"{oracle.get_num_threads()} OpenMP threads of {os.cpu_count()} host CPUs"}
+
+    def timed(seconds):
+        om.encode(ids[:chunk], mask[:chunk])           # warm-up
+        done, t0, i = 0, time.perf_counter(), 0
+        while True:
+            lo = (i * chunk) % spec.batch
+            om.encode(ids[lo:lo + chunk], mask[lo:lo + chunk])
+            done += chunk
+            i += 1
+            el = time.perf_counter() - t0
+            if el >= seconds:
+                return done, el
+
+    variants = {}
+    done, el = timed(budget_s / 2)
+    variants["default"] = {"value": round(done / el, 3), "sequences": done, "seconds": round(el, 1)}
+    blas = None
+    try:
+        blas = oracle.use_openblas(True)
+        done, el = timed(budget_s / 2)
+        variants["openblas"] = {"value": round(done / el, 3), "sequences": done,
+                                "seconds": round(el, 1), "library": os.path.basename(blas)}
+    except oracle.OracleError as e:
+        variants["openblas"] = {"value": None, "error": str(e)}
+    finally:
+        oracle.use_openblas(False)
+    best = max((k for k in variants if variants[k]["value"]), key=lambda k: variants[k]["value"])
+    n = oracle.get_num_threads()
+    return {"value": variants[best]["value"], "unit": "sentences/s", "cores": n, "kind": "port",
+            "sample": f"sequences of the {spec.name} workload (seq {spec.seq_len}) in chunks of "
+                      f"{chunk}, about {budget_s / 2:.0f} s per build, oracle/liboracle.so on {n} "
+                      f"OpenMP threads of {os.cpu_count()} host CPUs; value = the faster build "
+                      f"({best})",
+            "variants": variants}
 
 
 def text_path(model, spec, ids, mask, lengths, steps: int) -> dict:
@@ -171,8 +195,8 @@ def main():
     ap.add_argument("--config", default="c3", choices=["c1", "c2", "c3", "c4", "c5"])
     ap.add_argument("--dtype", default=None, help="fp32 | bf16 (default: the config's)")
     ap.add_argument("--profile-kernel", default="gemm_ffn_up", choices=KERNELS)
-    ap.add_argument("--cpu-budget", type=float, default=12.0,
-                    help="seconds of CPU baseline work (0 disables)")
+    ap.add_argument("--cpu-budget", type=float, default=16.0,
+                    help="seconds of CPU baseline work, split over its two builds (0 disables)")
     ap.add_argument("--host-api-steps", type=int, default=5,
                     help="blocking host-buffer forwards timed for host_api (0 disables)")
     ap.add_argument("--text-steps", type=int, default=5,

@@ -53,6 +53,7 @@ def lib():
         L.orc_cosine_similarity.argtypes = [_f32p, _f32p, ctypes.c_int]
         L.orc_dot.restype = ctypes.c_float
         L.orc_dot.argtypes = [_f32p, _f32p, ctypes.c_int]
+        L.orc_set_blas_sgemm.argtypes = [ctypes.c_void_p]
         L.orc_set_num_threads.argtypes = [ctypes.c_int]
         L.orc_get_num_threads.restype = ctypes.c_int
         _LIB = L
@@ -75,6 +76,48 @@ class OracleError(RuntimeError):
 def _check(rc: int):
     if rc != 0:
         raise OracleError(lib().orc_last_error().decode())
+
+
+_BLAS = None
+
+
+def openblas_sgemm():
+    """(path, address of cblas_sgemm, set_num_threads) of the OpenBLAS that
+    numpy links (ILP64, symbol suffix ``64_``), or None when there is none."""
+    global _BLAS
+    if _BLAS is None:
+        import glob
+        libs = os.path.join(os.path.dirname(os.path.dirname(np.__file__)), "numpy.libs")
+        found = ()
+        for path in sorted(glob.glob(os.path.join(libs, "libscipy_openblas64_*.so"))):
+            L = ctypes.CDLL(path)
+            try:
+                fn = ctypes.cast(L.scipy_cblas_sgemm64_, ctypes.c_void_p).value
+                nt = L.scipy_openblas_set_num_threads64_
+            except AttributeError:
+                continue
+            nt.argtypes = [ctypes.c_int]
+            found = (path, fn, nt)
+            break
+        _BLAS = found
+    return _BLAS or None
+
+
+def use_openblas(enabled: bool) -> str | None:
+    """Route every product of the oracle through OpenBLAS's cblas_sgemm (the
+    reference built with ``--features openblas``), or back to the built-in
+    sgemm.  OpenBLAS runs one thread per call; the batch slices spread over the
+    oracle's OpenMP threads.  Returns the library's path (None when disabled)."""
+    if not enabled:
+        lib().orc_set_blas_sgemm(None)
+        return None
+    b = openblas_sgemm()
+    if b is None:
+        raise OracleError("numpy's OpenBLAS (libscipy_openblas64_) was not found")
+    path, fn, nt = b
+    nt(1)
+    lib().orc_set_blas_sgemm(fn)
+    return path
 
 
 def set_num_threads(n: int):

@@ -14,6 +14,11 @@
  *     (bit-level parity unpinned, only tolerance-level parity is claimed);
  *   - ndarray 0.16 `sum` (eight-way unrolled fold) and `var_axis` (Welford with
  *     mul_add), used by mean_axis / var_axis / sum_axis.
+ * The reference's `openblas` feature (Cargo.toml:14, lib.rs:1-2) turns on
+ * ndarray's `blas` feature, which sends `.dot` to cblas_sgemm.  That variant is
+ * here too: orc_set_blas_sgemm() hands in a CBLAS (ILP64) sgemm, and every
+ * product then goes to it, one call per batch slice as `.dot` makes them, the
+ * slices spread over threads as the reference's rayon loops spread them.
  */
 #include "oracle.h"
 
@@ -38,6 +43,21 @@ static int fail(const char* fmt, ...) {
 const char* orc_last_error(void) { return g_err; }
 
 static int g_threads = 0;
+static orc_cblas_sgemm_fn g_blas = NULL;
+void orc_set_blas_sgemm(orc_cblas_sgemm_fn fn) { g_blas = fn; }
+
+/* c[m,n] = a[m,k] . b[k,n] through the CBLAS sgemm (row-major, no transposes,
+ * alpha 1, beta 0: ndarray's `dot` into a fresh array). */
+enum { CBLAS_ROW_MAJOR = 101, CBLAS_NO_TRANS = 111 };
+static void blas_dot(int m, int n, int k, const float* a, int lda, const float* b, int ldb,
+                     float* c, int ldc) {
+    if (k <= 0) {   /* an empty sum; CBLAS would reject lda = 0 */
+        for (int i = 0; i < m; ++i) memset(c + (size_t)i * ldc, 0, sizeof(float) * n);
+        return;
+    }
+    g_blas(CBLAS_ROW_MAJOR, CBLAS_NO_TRANS, CBLAS_NO_TRANS, m, n, k, 1.0f, a, lda, b, ldb, 0.0f,
+           c, ldc);
+}
 void orc_set_num_threads(int n) { g_threads = n > 0 ? n : 0; if (n > 0) omp_set_num_threads(n); }
 int orc_get_num_threads(void) { return g_threads > 0 ? g_threads : omp_get_max_threads(); }
 
@@ -157,6 +177,10 @@ static void gemm_packed_serial(int m, int n, int k, const float* a, int lda, con
 void orc_sgemm(int m, int n, int k, const float* a, int lda, const float* b, int ldb, float* c,
                int ldc) {
     if (m <= 0 || n <= 0) return;
+    if (g_blas) {
+        blas_dot(m, n, k, a, lda, b, ldb, c, ldc);
+        return;
+    }
     if (k <= 0) {
         for (int i = 0; i < m; ++i) memset(c + (size_t)i * ldc, 0, sizeof(float) * n);
         return;
@@ -180,6 +204,12 @@ void orc_sgemm(int m, int n, int k, const float* a, int lda, const float* b, int
  * sequential over slices when batch <= 4, parallel over slices otherwise.
  * w is packed once and shared by every slice. */
 void orc_matmul_3d_2d(const float* a, int batch, int m, int k, const float* b, int n, float* c) {
+    if (g_blas) {
+#pragma omp parallel for schedule(dynamic, 1) if (batch > 4)
+        for (int s = 0; s < batch; ++s)
+            blas_dot(m, n, k, a + (size_t)s * m * k, k, b, n, c + (size_t)s * m * n, n);
+        return;
+    }
     if (batch <= 4) {
         for (int s = 0; s < batch; ++s)
             orc_sgemm(m, n, k, a + (size_t)s * m * k, k, b, n, c + (size_t)s * m * n, n);
@@ -199,6 +229,13 @@ void orc_matmul_3d_2d(const float* a, int batch, int m, int k, const float* b, i
 void orc_matmul_4d(const float* a, const float* b, int batch, int heads, int seq1, int dim,
                    int seq2, float* c) {
     int total = batch * heads;
+    if (g_blas) {
+#pragma omp parallel for schedule(dynamic, 4) if (total > 8)
+        for (int t = 0; t < total; ++t)
+            blas_dot(seq1, seq2, dim, a + (size_t)t * seq1 * dim, dim, b + (size_t)t * dim * seq2,
+                     seq2, c + (size_t)t * seq1 * seq2, seq2);
+        return;
+    }
     if (total <= 8) {
         for (int t = 0; t < total; ++t)
             orc_sgemm(seq1, seq2, dim, a + (size_t)t * seq1 * dim, dim,

@@ -39,6 +39,15 @@ const char* orc_last_error(void);
 void orc_set_num_threads(int n);
 int orc_get_num_threads(void);
 
+/* The reference's `openblas` feature (Cargo.toml:14): every `.dot` goes to
+ * cblas_sgemm.  fn has the ILP64 CBLAS signature; NULL restores the built-in
+ * sgemm (the default feature set, matrixmultiply). */
+typedef void (*orc_cblas_sgemm_fn)(int order, int trans_a, int trans_b, int64_t m, int64_t n,
+                                   int64_t k, float alpha, const float* a, int64_t lda,
+                                   const float* b, int64_t ldb, float beta, float* c,
+                                   int64_t ldc);
+void orc_set_blas_sgemm(orc_cblas_sgemm_fn fn);
+
 orc_model* orc_model_new(int hidden_size, int num_attention_heads, int num_hidden_layers,
                          int intermediate_size, int vocab_size, int max_position_embeddings,
                          int type_vocab_size, float layer_norm_eps);

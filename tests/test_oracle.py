@@ -16,6 +16,8 @@ formula:
 
 CPU only (no GPU marker).
 """
+import os
+
 import numpy as np
 import pytest
 
@@ -89,6 +91,58 @@ def test_matmul_4d_vs_numpy(B, h):
     b = RNG.standard_normal((B, h, 5, 13)).astype(np.float32)
     np.testing.assert_allclose(oracle.matmul_4d(a, b), a.astype(np.float64) @ b, rtol=1e-5,
                                atol=1e-5)
+
+
+@pytest.fixture
+def openblas():
+    """The oracle with every product on OpenBLAS's cblas_sgemm (the reference's
+    ``openblas`` feature), restored to the built-in sgemm afterwards."""
+    if oracle.openblas_sgemm() is None:
+        pytest.skip("numpy links no ILP64 OpenBLAS here")
+    oracle.use_openblas(True)
+    yield
+    oracle.use_openblas(False)
+
+
+@pytest.mark.parametrize("m,n,k", [(7, 19, 13), (130, 384, 1536), (3, 5, 0)])
+def test_sgemm_openblas_vs_numpy(openblas, m, n, k):
+    a = RNG.standard_normal((m, k)).astype(np.float32)
+    b = RNG.standard_normal((k, n)).astype(np.float32)
+    np.testing.assert_allclose(oracle.sgemm(a, b), a.astype(np.float64) @ b.astype(np.float64),
+                               rtol=1e-5, atol=1e-5 * np.sqrt(max(k, 1)))
+
+
+@pytest.mark.parametrize("batch", [4, 9])
+def test_matmuls_openblas_vs_numpy(openblas, batch):
+    """Both matmul_3d_2d and matmul_4d branches (sequential / over threads)."""
+    a = RNG.standard_normal((batch, 11, 24)).astype(np.float32)
+    w = RNG.standard_normal((24, 40)).astype(np.float32)
+    np.testing.assert_allclose(oracle.matmul_3d_2d(a, w), a.astype(np.float64) @ w, rtol=1e-5,
+                               atol=1e-5)
+    q = RNG.standard_normal((batch, 3, 9, 5)).astype(np.float32)
+    k = RNG.standard_normal((batch, 3, 5, 13)).astype(np.float32)
+    np.testing.assert_allclose(oracle.matmul_4d(q, k), q.astype(np.float64) @ k, rtol=1e-5,
+                               atol=1e-5)
+
+
+def test_openblas_variant_encodes_like_the_default(weights_for):
+    """The whole encoder with OpenBLAS products: the same vectors as with the
+    built-in sgemm to summation-order noise, and the golden c2 vectors."""
+    if oracle.openblas_sgemm() is None:
+        pytest.skip("numpy links no ILP64 OpenBLAS here")
+    spec = synth.CONFIGS["c2"]
+    ids, mask, _ = synth.make_inputs(spec)
+    om = oracle.OracleModel(spec.model, weights_for(spec.model))
+    want = om.encode(ids[:8], mask[:8])
+    oracle.use_openblas(True)
+    try:
+        got = om.encode(ids[:8], mask[:8])
+    finally:
+        oracle.use_openblas(False)
+    assert np.abs(got - want).max() <= 1e-6
+    with np.load(os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden",
+                              "encoder_golden.npz"), allow_pickle=False) as z:
+        np.testing.assert_allclose(got, z["c2_out"], rtol=0, atol=1e-6)
 
 
 def test_softmax_vs_torch():
