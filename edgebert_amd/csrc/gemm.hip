@@ -244,7 +244,10 @@ constexpr int BUFFER_RSRC_WORD3 = 0x00020000;
 // BF16: A and W are bf16 (16-byte chunk = 8 elements, one
 // v_mfma_f32_32x32x16_bf16 per fragment pair and k-slice); otherwise fp32
 // (chunk = 4 elements, four v_mfma_f32_32x32x2_f32).  OUT16: C is written as
-// bf16 (round to nearest even) instead of fp32.  LDS offsets below are in
+// bf16 (round to nearest even) instead of fp32, through the packed epilogue:
+// the MFMAs take W as their first operand, so each block holds C transposed
+// and a lane holds four consecutive columns of one C row per group of four
+// accumulators (epilogue_packed).  LDS offsets below are in
 // 4-byte words, so both element types share the layout and the swizzle.
 template <bool BF16, bool OUT16, int BM, int BN, int BK, int WAVES_M, int WAVES_N, int NSTAGE, int EPI,
           bool SPREAD = BF16>
@@ -272,12 +275,14 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_persistent_kernel
     // FLAT: wave tiles too wide for a 32-row transpose per stage, or whose
     // float4 rows do not tile 64 lanes (e.g. 96 columns): C goes through LDS
     // 16 rows at a time and the lanes walk the rows' float4 in order.
-    constexpr bool FLAT = !LN && (64 % C4 != 0 || NW * 32 * WN > STAGE);
-    static_assert(LN || FLAT || NW * 32 * WN <= STAGE, "each wave transposes 32 C rows at a time through one stage");
+    constexpr bool PACKED = OUT16;
+    static_assert(!PACKED || (NW * 16 * WN <= STAGE && WN % 64 == 0), "packed epilogue: 32 bf16 rows per wave per stage");
+    constexpr bool FLAT = !LN && !PACKED && (64 % C4 != 0 || NW * 32 * WN > STAGE);
+    static_assert(LN || FLAT || PACKED || NW * 32 * WN <= STAGE, "each wave transposes 32 C rows at a time through one stage");
     static_assert(!FLAT || (NW * 16 * WN <= STAGE && (4 * WN) % 64 == 0), "16-row transpose shape");
     static_assert(!LN || 2 * WAVES_N * BM + 2 * NW * 64 <= STAGE, "LayerNorm exchange fits one stage");
     constexpr int RPP = FLAT || LN ? 1 : 64 / C4; // wave-tile rows per float4 pass
-    static_assert(LN || FLAT || (C4 * RPP == 64 && 32 % RPP == 0), "epilogue pass shape");
+    static_assert(LN || FLAT || PACKED || (C4 * RPP == 64 && 32 % RPP == 0), "epilogue pass shape");
     constexpr int NPB = 32 / RPP;                 // float4 passes per 32-row block
     constexpr int BIAS_SLOT = 256;                // floats: one wave's 64 x 16-byte bias chunks
 
@@ -600,8 +605,61 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_persistent_kernel
         }
     };
 
+    // Packed bf16 epilogue.  acc[i][j][4g + e] is C at row i*32 + l32 and
+    // column j*32 + 8g + 4*half + e of the wave tile: four consecutive columns,
+    // which get their bias (+ GELU) and are rounded into one 8-byte pair of
+    // bf16 words.  Per 32-row block, the wave's 32 rows x WN bf16 go through
+    // its slot of LDS stage `cs` (16-byte chunk c of row r at c ^ (r & 7), so
+    // neither the 8-byte writes down a column nor the 16-byte reads along the
+    // rows collide on a bank) and leave as 16-byte row-contiguous stores.
+    auto epilogue_packed = [&](int t, const float* cs_base) __attribute__((always_inline)) {
+        const int u = wg + t * G, split = u / ntiles, tile = u - split * ntiles;
+        uint16_t* const Cs = reinterpret_cast<uint16_t*>(p.C) + (int64_t)split * p.split_stride;
+        const int m0 = (tile / ntiles_n) * BM, n0 = (tile - (tile / ntiles_n) * ntiles_n) * BN;
+        const float* bslot = smem + NSTAGE * STAGE + ((t & 1) * NW + wave) * BIAS_SLOT;
+        char* cw = reinterpret_cast<char*>(const_cast<float*>(cs_base) + wave * (16 * WN));
+        constexpr int CPW = WN / 8;               // 16-byte chunks per wave-tile row
+        constexpr int NPASS = 32 * CPW / 64;
+        const bool wide = (p.ldc & 7) == 0;       // rows 16-byte aligned
+#pragma unroll
+        for (int i = 0; i < FM; ++i) {
+#pragma unroll
+            for (int j = 0; j < FN; ++j)
+#pragma unroll
+                for (int g = 0; g < 4; ++g) {
+                    float4 v = make_float4(acc[i][j][4 * g], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2], acc[i][j][4 * g + 3]);
+                    if (HAS_BIAS) {
+                        const float4 b4 = *reinterpret_cast<const float4*>(bslot + j * 32 + 8 * g + 4 * half);
+                        v.x += b4.x; v.y += b4.y; v.z += b4.z; v.w += b4.w;
+                    }
+                    if constexpr (EPI == EPI_BIAS_GELU) {
+                        v.x = gelu_tanh_fast(v.x); v.y = gelu_tanh_fast(v.y);
+                        v.z = gelu_tanh_fast(v.z); v.w = gelu_tanh_fast(v.w);
+                    }
+                    const uint2 h = make_uint2(pack_bf16x2(v.x, v.y), pack_bf16x2(v.z, v.w));
+                    *reinterpret_cast<uint2*>(cw + l32 * (2 * WN) + (((j * 4 + g) ^ (l32 & 7)) << 4) + 8 * half) = h;
+                }
+#pragma unroll
+            for (int ps = 0; ps < NPASS; ++ps) {
+                const int q = ps * 64 + lane, r = q / CPW, c = q - r * CPW;
+                const uint4 d = *reinterpret_cast<const uint4*>(cw + r * (2 * WN) + ((c ^ (r & 7)) << 4));
+                const int grow = m0 + wm * WM + i * 32 + r, gcol = n0 + wn * WN + 8 * c;
+                if (grow < M && gcol < N) {   // N % 4 == 0: the chunk's first 4 columns are in
+                    uint16_t* dst = Cs + (int64_t)grow * p.ldc + gcol;
+                    if (wide && gcol + 8 <= N) {
+                        *reinterpret_cast<uint4*>(dst) = d;
+                    } else {
+                        *reinterpret_cast<uint2*>(dst) = make_uint2(d.x, d.y);
+                        if (gcol + 8 <= N) *reinterpret_cast<uint2*>(dst + 4) = make_uint2(d.z, d.w);
+                    }
+                }
+            }
+        }
+    };
+
     auto finish_tile = [&](int t, float* stage) __attribute__((always_inline)) {
         if constexpr (LN) epilogue_ln(t, stage);
+        else if constexpr (PACKED) epilogue_packed(t, stage);
         else if constexpr (FLAT) epilogue_flat(t, stage);
         else epilogue_tile(t, stage);
     };
@@ -649,8 +707,11 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_persistent_kernel
                     for (int i = 0; i < FM; ++i)
 #pragma unroll
                         for (int j = 0; j < FN; ++j)
-                            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
-                                __builtin_bit_cast(v8bf, af[i]), __builtin_bit_cast(v8bf, wf[j]), acc[i][j], 0, 0, 0);
+                            acc[i][j] = PACKED
+                                ? __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+                                      __builtin_bit_cast(v8bf, wf[j]), __builtin_bit_cast(v8bf, af[i]), acc[i][j], 0, 0, 0)
+                                : __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+                                      __builtin_bit_cast(v8bf, af[i]), __builtin_bit_cast(v8bf, wf[j]), acc[i][j], 0, 0, 0);
                 } else {
 #pragma unroll
                     for (int q = 0; q < 4; ++q)
@@ -658,8 +719,9 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_persistent_kernel
                         for (int i = 0; i < FM; ++i)
 #pragma unroll
                             for (int j = 0; j < FN; ++j)
-                                acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(af[i][q], wf[j][q],
-                                                                                 acc[i][j], 0, 0, 0);
+                                acc[i][j] = PACKED
+                                    ? __builtin_amdgcn_mfma_f32_32x32x2f32(wf[j][q], af[i][q], acc[i][j], 0, 0, 0)
+                                    : __builtin_amdgcn_mfma_f32_32x32x2f32(af[i][q], wf[j][q], acc[i][j], 0, 0, 0);
                 }
             }
         }

@@ -206,4 +206,13 @@ __device__ __forceinline__ uint16_t f32_to_bf16_rne(float f) {
     return (uint16_t)(u >> 16);
 }
 
+// Two floats to two bf16 (round to nearest even, NaN stays NaN) packed in one
+// word, lo in bits 0..15: gfx950's v_cvt_pk_bf16_f32.
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+    typedef float v2f_t __attribute__((ext_vector_type(2)));
+    typedef __bf16 v2bf_t __attribute__((ext_vector_type(2)));
+    const v2f_t v = {lo, hi};
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, v2bf_t));
+}
+
 }  // namespace ebh
