@@ -2,10 +2,13 @@
 
 One step = one ``ebh_encode_device`` forward of the whole batch (embeddings ->
 L layers -> mean pool -> L2 normalise) over ids / mask already resident in
-HBM, ending with the stream synchronised.  Default workload: c3, MiniLM-L6
+HBM, ending with the stream synchronised.  From the second call on, a forward
+of the same shape on the same buffers replays as a HIP graph (the library's
+default; ``--no-graph-replay`` times direct launches).  Default workload: c3, MiniLM-L6
 shape, batch 256 x seq 128, fp32, seeded synthetic ids, random-init weights.
 
-Prints one JSON line.  ``roofline`` is measured live for one kernel family
+Prints one JSON line.  ``roofline`` is measured live, over as many forwards
+again right after the timed region, for one kernel family
 (default: the FFN-up GEMM, the largest single launch) with HIP events on the
 stream its launches go to; its ``traffic`` (HBM bytes per launch) is read from
 the committed rocprofv3 counter summary for the same workload and kernel, when
@@ -201,6 +204,8 @@ def main():
                     help="blocking host-buffer forwards timed for host_api (0 disables)")
     ap.add_argument("--text-steps", type=int, default=5,
                     help="batches timed for encode_texts and the tokenizers (0 disables)")
+    ap.add_argument("--no-graph-replay", action="store_true",
+                    help="run every forward as direct launches (no HIP graph replay)")
     ap.add_argument("--copy-probe-mb", type=int, default=0,
                     help="after the timed region, run 3 plain device copies of this many MiB "
                          "(the calibration dispatch for rocprofv3 FETCH_SIZE / WRITE_SIZE)")
@@ -232,22 +237,33 @@ def main():
         model.encode_device(d_ids.data_ptr(), d_mask.data_ptr(), B, S, d_out.data_ptr(),
                             True, stream)
 
+    if args.no_graph_replay:
+        model.set_graph_replay(False)
     for _ in range(args.warmup):
         step()
     model.synchronize()
     torch.cuda.synchronize()
 
-    model.profile_enable(args.profile_kernel)
-    times = []
-    torch.cuda.synchronize()
-    t_all = time.perf_counter()
-    for _ in range(args.steps):
-        t0 = time.perf_counter()
-        step()
+    def timed(n):
+        times = []
         torch.cuda.synchronize()
-        times.append(time.perf_counter() - t0)
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - t_all
+        t_all = time.perf_counter()
+        for _ in range(n):
+            t0 = time.perf_counter()
+            step()
+            torch.cuda.synchronize()
+            times.append(time.perf_counter() - t0)
+        torch.cuda.synchronize()
+        return time.perf_counter() - t_all, times
+
+    # The timed region: forwards as a caller runs them (graph replay on unless
+    # --no-graph-replay).  Then the same number of forwards with one kernel
+    # family timed by HIP events on its stream (those run as direct launches)
+    # for the roofline.
+    wall, times = timed(args.steps)
+    model.synchronize()
+    model.profile_enable(args.profile_kernel)
+    timed(args.steps)
     model.synchronize()
     launches, prof_ms = model.profile_read()
     model.profile_enable("none")
@@ -285,6 +301,7 @@ def main():
                    "global_batch": B, "seq_len": S, "valid_tokens": tokens,
                    "parallelism": "single GPU"},
         "forward_tflops": round(fwd_flops / (ms_per_step * 1e-3) / 1e12, 2),
+        "graph_replay": not args.no_graph_replay,
         "roofline": {"kernel": args.profile_kernel, "bound": bound, "achieved": round(achieved, 3),
                      "peak": peak, "unit": punit, "frac": round(achieved / peak, 4),
                      "traffic": measured_traffic(args.config, args.profile_kernel, dtype),

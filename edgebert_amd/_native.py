@@ -59,6 +59,7 @@ _SIGS = {
     "ebh_score": (_i32, [_vp, _vp, _vp, _i32, _i32, _vp]),
     "ebh_score_device": (_i32, [_vp, _vp, _vp, _i32, _i32, _vp, _vp]),
     "ebh_synchronize": (_i32, [_vp]),
+    "ebh_set_graph_replay": (_i32, [_vp, _i32]),
     "ebh_tokenizer_load": (_i32, [ctypes.c_char_p, ctypes.POINTER(_vp)]),
     "ebh_tokenizer_from_json": (_i32, [ctypes.c_char_p, ctypes.c_size_t, ctypes.POINTER(_vp)]),
     "ebh_tokenizer_destroy": (None, [_vp]),

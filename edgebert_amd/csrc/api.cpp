@@ -9,6 +9,7 @@
 //   up GEMM(+GELU), down GEMM(+res), LN] -> pool(+normalise).
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
@@ -80,6 +81,19 @@ struct ProfPair {
     hipEvent_t a, b;
 };
 
+// A whole forward recorded as a HIP graph, for calls that repeat one shape on
+// the same buffers (serving loops, small batches whose forward is mostly
+// launch overhead).  Keyed by everything the recorded launches bake in.
+struct GraphEntry {
+    int B, S, normalize, host;
+    const void *ids, *mask;
+    void *out, *scores;
+    int seen;                         // calls with this key; -1: recording failed
+    hipGraphExec_t exec;              // recorded at the key's second call
+    uint64_t used;
+};
+constexpr size_t MAX_GRAPHS = 16;
+
 }  // namespace
 
 struct ebh_model {
@@ -106,6 +120,10 @@ struct ebh_model {
     float* h_out = nullptr;
     int* h_err = nullptr;
     int64_t h_cap = 0, h_out_cap = 0;
+    // recorded forwards (GraphEntry), least recently used dropped first
+    std::vector<GraphEntry> graphs;
+    uint64_t graph_clock = 0;
+    bool graph_replay = true;
     // profiling of one kernel family
     int prof_kind = EBH_PROF_NONE;
     std::vector<ProfPair> prof_events;
@@ -199,6 +217,12 @@ void prof_end(ebh_model* m, hipStream_t s, ProfPair& pp, bool on) {
     m->prof_events.push_back(pp);
 }
 
+void drop_graphs(ebh_model* m) {
+    for (auto& g : m->graphs)
+        if (g.exec) (void)hipGraphExecDestroy(g.exec);
+    m->graphs.clear();
+}
+
 int ensure_workspace(ebh_model* m, int B, int S) {
     const int64_t T = (int64_t)B * S;
     Workspace& w = m->ws;
@@ -221,8 +245,10 @@ int ensure_workspace(ebh_model* m, int B, int S) {
                  oMask = take(tcap * 4), oCounts = take(bcap * 4), oCu = take((bcap + 1) * 4),
                  oNtok = take(4), oTid = take(tcap * 4), oTpos = take(tcap * 4), oErr = take(4),
                  oOut = take((size_t)bcap * H * 4), oScores = take((size_t)bcap * 4);
-    // Work from the previous call may still use the old block.
+    // Work from the previous call may still use the old block, and recorded
+    // forwards hold its addresses.
     if (m->has_done) HIP_TRY(hipEventSynchronize(m->done));
+    drop_graphs(m);
     if (w.base) HIP_TRY(hipFree(w.base));
     w.base = nullptr;
     w.tok_cap = 0;
@@ -255,6 +281,11 @@ int ensure_workspace(ebh_model* m, int B, int S) {
 }
 
 int ensure_host_staging(ebh_model* m, int64_t T, int64_t outn) {
+    if (T > m->h_cap || outn > m->h_out_cap) {
+        // Recorded host-path forwards copy from / to these buffers.
+        if (m->has_done) HIP_TRY(hipEventSynchronize(m->done));
+        drop_graphs(m);
+    }
     if (T > m->h_cap) {
         if (m->h_ids) (void)hipHostFree(m->h_ids);
         if (m->h_mask) (void)hipHostFree(m->h_mask);
@@ -275,11 +306,11 @@ int ensure_host_staging(ebh_model* m, int64_t T, int64_t outn) {
     return EBH_OK;
 }
 
-// Enqueue the whole forward on stream s (ids/mask already in device memory).
+// The kernels of one forward on stream s (ids/mask already in device memory).
 // d_scores (optional, cross-encoders): score[b] = pooled[b] . w + bias, from
 // the un-normalised pooled rows left in d_out.
-int enqueue_forward(ebh_model* m, const int* d_ids, const int* d_mask, int B, int S,
-                    int normalize, float* d_out, hipStream_t s, float* d_scores = nullptr) {
+int enqueue_kernels(ebh_model* m, const int* d_ids, const int* d_mask, int B, int S,
+                    int normalize, float* d_out, hipStream_t s, float* d_scores) {
     const ebh_config& c = m->cfg;
     const int H = c.hidden_size, I = c.intermediate_size, nh = c.num_attention_heads;
     const int hd = H / nh;
@@ -287,7 +318,6 @@ int enqueue_forward(ebh_model* m, const int* d_ids, const int* d_mask, int B, in
     const float scale = 1.0f / sqrtf((float)hd);  // src/lib.rs:196-197
     Workspace& w = m->ws;
     const int T = B * S;
-    if (m->has_done) HIP_TRY(hipStreamWaitEvent(s, m->done, 0));
 
     ProfPair pp{};
     bool on = false;
@@ -425,6 +455,86 @@ int enqueue_forward(ebh_model* m, const int* d_ids, const int* d_mask, int B, in
     HIP_TRY(ebh::launch_pool(w.X, w.cu, B, H, S, normalize, d_out, s));
     prof_end(m, s, pp, on);
     if (d_scores) HIP_TRY(ebh::launch_cls_head(d_out, m->cls_w, m->cls_b, B, H, d_scores, s));
+    return EBH_OK;
+}
+
+// The recorded forward for this call, recording it at the key's second call;
+// nullptr: run the launches directly (replay off, profiling on, the caller's
+// stream being captured into a graph of its own, or recording failed).
+template <class Body>
+hipGraphExec_t graph_for(ebh_model* m, const GraphEntry& key, hipStream_t s, Body&& body) {
+    if (!m->graph_replay || m->prof_kind != EBH_PROF_NONE) return nullptr;
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(s, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone) return nullptr;
+    GraphEntry* e = nullptr;
+    for (auto& g : m->graphs)
+        if (g.B == key.B && g.S == key.S && g.normalize == key.normalize && g.host == key.host &&
+            g.ids == key.ids && g.mask == key.mask && g.out == key.out && g.scores == key.scores) {
+            e = &g;
+            break;
+        }
+    if (!e) {
+        if (m->graphs.size() >= MAX_GRAPHS) {
+            auto lru = std::min_element(m->graphs.begin(), m->graphs.end(),
+                                        [](const GraphEntry& a, const GraphEntry& b) { return a.used < b.used; });
+            if (lru->exec) (void)hipGraphExecDestroy(lru->exec);
+            m->graphs.erase(lru);
+        }
+        m->graphs.push_back(key);
+        m->graphs.back().seen = 1;
+        m->graphs.back().exec = nullptr;
+        m->graphs.back().used = ++m->graph_clock;
+        return nullptr;
+    }
+    e->used = ++m->graph_clock;
+    if (e->exec || e->seen < 0) return e->exec;
+    // Record on the model's own stream (never the legacy default stream);
+    // the graph is then launched on s.
+    hipGraph_t g = nullptr;
+    bool ok = hipStreamBeginCapture(m->stream, hipStreamCaptureModeThreadLocal) == hipSuccess;
+    if (ok) {
+        const int rc = body(m->stream);
+        ok = hipStreamEndCapture(m->stream, &g) == hipSuccess && rc == EBH_OK && g &&
+             hipGraphInstantiate(&e->exec, g, nullptr, nullptr, 0) == hipSuccess;
+    }
+    if (g) (void)hipGraphDestroy(g);
+    if (!ok) {
+        e->exec = nullptr;
+        e->seen = -1;
+        (void)hipGetLastError();
+    }
+    return e->exec;
+}
+
+// One forward on stream s, ordered after the model's previous work.  host:
+// ids / mask come from the pinned staging buffers and the result (d_scores
+// if given, else d_out) and the id-range flag go back to them.
+int run_forward(ebh_model* m, const int* d_ids, const int* d_mask, int B, int S, int normalize,
+                float* d_out, hipStream_t s, float* d_scores, bool host) {
+    Workspace& w = m->ws;
+    const int64_t T = (int64_t)B * S;
+    const size_t n_out = d_scores ? (size_t)B : (size_t)B * m->cfg.hidden_size;
+    if (m->has_done) HIP_TRY(hipStreamWaitEvent(s, m->done, 0));
+    auto body = [&](hipStream_t st) -> int {
+        if (host) {
+            HIP_TRY(hipMemcpyAsync(w.ids, m->h_ids, T * 4, hipMemcpyHostToDevice, st));
+            HIP_TRY(hipMemcpyAsync(w.mask, m->h_mask, T * 4, hipMemcpyHostToDevice, st));
+        }
+        int rc = enqueue_kernels(m, d_ids, d_mask, B, S, normalize, d_out, st, d_scores);
+        if (rc) return rc;
+        if (host) {
+            HIP_TRY(hipMemcpyAsync(m->h_out, d_scores ? d_scores : d_out, n_out * 4, hipMemcpyDeviceToHost, st));
+            HIP_TRY(hipMemcpyAsync(m->h_err, w.err, 4, hipMemcpyDeviceToHost, st));
+        }
+        return EBH_OK;
+    };
+    const GraphEntry key{B, S, normalize, host ? 1 : 0, d_ids, d_mask, d_out, d_scores, 0, nullptr, 0};
+    if (hipGraphExec_t exec = graph_for(m, key, s, body)) {
+        HIP_TRY(hipGraphLaunch(exec, s));
+    } else {
+        const int rc = body(s);
+        if (rc) return rc;
+    }
     HIP_TRY(hipEventRecord(m->done, s));
     m->has_done = true;
     m->last_B = B;
@@ -435,20 +545,14 @@ int enqueue_forward(ebh_model* m, const int* d_ids, const int* d_mask, int B, in
 // Staged host ids / mask -> device forward -> out ([B, H], or the [B]
 // cross-encoder scores when `score`).
 int forward_host_staged(ebh_model* m, int B, int S, int normalize, float* out, bool score = false) {
-    const int64_t T = (int64_t)B * S;
     const int H = m->cfg.hidden_size;
     const size_t n_out = score ? (size_t)B : (size_t)B * H;
     hipStream_t s = m->stream;
     int rc = ensure_workspace(m, B, S);
     if (rc) return rc;
-    if (m->has_done) HIP_TRY(hipStreamWaitEvent(s, m->done, 0));
-    HIP_TRY(hipMemcpyAsync(m->ws.ids, m->h_ids, T * 4, hipMemcpyHostToDevice, s));
-    HIP_TRY(hipMemcpyAsync(m->ws.mask, m->h_mask, T * 4, hipMemcpyHostToDevice, s));
-    if ((rc = enqueue_forward(m, m->ws.ids, m->ws.mask, B, S, normalize, m->ws.out, s,
-                              score ? m->ws.scores : nullptr)))
+    if ((rc = run_forward(m, m->ws.ids, m->ws.mask, B, S, normalize, m->ws.out, s,
+                          score ? m->ws.scores : nullptr, true)))
         return rc;
-    HIP_TRY(hipMemcpyAsync(m->h_out, score ? m->ws.scores : m->ws.out, n_out * 4, hipMemcpyDeviceToHost, s));
-    HIP_TRY(hipMemcpyAsync(m->h_err, m->ws.err, 4, hipMemcpyDeviceToHost, s));
     HIP_TRY(hipStreamSynchronize(s));
     if (*m->h_err) return fail(EBH_ERR_RANGE, "token id out of range for vocab %d", m->cfg.vocab_size);
     memcpy(out, m->h_out, n_out * 4);
@@ -665,6 +769,7 @@ void ebh_destroy(ebh_model* m) {
         if (m->stream) (void)hipStreamSynchronize(m->stream);
         for (auto& p : m->prof_events) { (void)hipEventDestroy(p.a); (void)hipEventDestroy(p.b); }
         for (auto& e : m->prof_free) (void)hipEventDestroy(e);
+        drop_graphs(m);
         if (m->ws.base) (void)hipFree(m->ws.base);
         if (m->wbase) (void)hipFree(m->wbase);
         if (m->h_ids) (void)hipHostFree(m->h_ids);
@@ -755,7 +860,7 @@ int ebh_encode_device(ebh_model* m, const int32_t* ids, const int32_t* mask, int
         return EBH_OK;
     }
     if ((rc = ensure_workspace(m, B, S))) return rc;
-    return enqueue_forward(m, ids, mask, B, S, normalize ? 1 : 0, out, s);
+    return run_forward(m, ids, mask, B, S, normalize ? 1 : 0, out, s, nullptr, false);
 }
 
 int ebh_score(ebh_model* m, const uint32_t* ids, const uint32_t* mask, int32_t B, int32_t S,
@@ -850,7 +955,7 @@ int ebh_score_device(ebh_model* m, const int32_t* ids, const int32_t* mask, int3
     HIP_TRY(hipSetDevice(m->device));
     hipStream_t s = stream ? static_cast<hipStream_t>(stream) : m->stream;
     if ((rc = ensure_workspace(m, B, S))) return rc;
-    return enqueue_forward(m, ids, mask, B, S, 0, m->ws.out, s, scores);
+    return run_forward(m, ids, mask, B, S, 0, m->ws.out, s, scores, false);
 }
 
 int ebh_synchronize(ebh_model* m) {
@@ -896,6 +1001,19 @@ int ebh_model_info(const ebh_model* m, ebh_config* cfg_out, int32_t* dtype_out) 
     if (!m) return fail(EBH_ERR_INVALID_ARG, "null model");
     if (cfg_out) *cfg_out = m->cfg;
     if (dtype_out) *dtype_out = m->dtype;
+    return EBH_OK;
+}
+
+int ebh_set_graph_replay(ebh_model* m, int32_t enable) {
+    int rc = check_model_ready(m);
+    if (rc) return rc;
+    std::lock_guard<std::mutex> lk(m->mu);
+    HIP_TRY(hipSetDevice(m->device));
+    m->graph_replay = enable != 0;
+    if (!m->graph_replay) {
+        if (m->has_done) HIP_TRY(hipEventSynchronize(m->done));
+        drop_graphs(m);
+    }
     return EBH_OK;
 }
 

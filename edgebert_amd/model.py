@@ -290,6 +290,11 @@ class Model:
     def synchronize(self):
         N.check(N.lib().ebh_synchronize(self._h))
 
+    def set_graph_replay(self, enable: bool):
+        """Record repeated forwards (same shape and buffers) as HIP graphs and
+        replay them (default on); off runs every launch directly."""
+        N.check(N.lib().ebh_set_graph_replay(self._h, 1 if enable else 0))
+
     def last_tokens(self, B: int):
         n = ctypes.c_int32()
         N.check(N.lib().ebh_last_tokens(self._h, None, None, 0, None, 0, ctypes.byref(n)))

@@ -182,6 +182,20 @@ EBH_API int ebh_score_texts(ebh_model* m, const ebh_tokenizer* t, const char* co
                     const int64_t* q_lens, const char* const* documents, const int64_t* d_lens,
                     int32_t n, float* scores, int32_t nthreads);
 
+/* Graph replay (no counterpart in the reference, whose forward runs on the
+ * CPU; for serving loops and small batches, whose forward is mostly launch
+ * overhead).  When on (the default), the second forward with the same batch
+ * shape, normalize flag and buffers (ebh_encode / ebh_forward / ebh_score /
+ * the text entry points: the model's own staging; the _device entry points:
+ * the caller's pointers) is recorded as a HIP graph, and every later one
+ * replays it: the same kernels with the same arguments, so results are
+ * bit-identical to direct launches.  Up to 16 recordings per model, least
+ * recently used dropped first; all are dropped when the model's buffers grow.
+ * Forwards run directly while a kernel is being profiled or while the
+ * caller's stream is itself being captured.  enable = 0 turns replay off and
+ * frees the recordings. */
+EBH_API int ebh_set_graph_replay(ebh_model* m, int32_t enable);
+
 /* Wait for the model's outstanding work; EBH_ERR_RANGE if a device-side id
  * check failed since the previous ebh_synchronize / blocking call. */
 EBH_API int ebh_synchronize(ebh_model* m);
