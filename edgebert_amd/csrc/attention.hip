@@ -31,7 +31,7 @@ typedef float v16f __attribute__((ext_vector_type(16)));
 typedef float v4f __attribute__((ext_vector_type(4)));
 
 template <int HD>
-__global__ __launch_bounds__(256) void attention_kernel(const float* __restrict__ qkv,
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(HD == 32 ? 3 : 2))) void attention_kernel(const float* __restrict__ qkv,
                                                         const int* __restrict__ cu_seqlens,
                                                         float* __restrict__ ctx_out, int H,
                                                         float scale) {
@@ -72,17 +72,31 @@ __global__ __launch_bounds__(256) void attention_kernel(const float* __restrict_
     for (int c = 0; c < nchunks; ++c) {
         const int kbase = c * KC;
         __syncthreads();  // previous chunk fully consumed
-        constexpr int F4 = KC * HD / 4;
-        for (int i = tid; i < F4; i += 256) {
-            const int r = i / (HD / 4), cc = i % (HD / 4);
-            const int key = kbase + r;
-            float4 kv = make_float4(0, 0, 0, 0), vv = make_float4(0, 0, 0, 0);
-            if (key < len) {
-                kv = *reinterpret_cast<const float4*>(Kg + (int64_t)key * ld + cc * 4);
-                vv = *reinterpret_cast<const float4*>(Vg + (int64_t)key * ld + cc * 4);
+        // K and V loads go out in groups of up to 4 + 4 float4 per thread, a
+        // group's loads all issued before its LDS writes: the chunk costs one
+        // or two memory round trips instead of one per piece.
+        constexpr int F4 = KC * HD / 4;       // float4 pieces of K (and of V)
+        constexpr int PT = F4 / 256;          // per thread
+        constexpr int GP = PT < 4 ? PT : 4;   // per group
+        static_assert(PT * 256 == F4 && PT % GP == 0, "whole pieces per thread");
+#pragma unroll
+        for (int g0 = 0; g0 < PT; g0 += GP) {
+            float4 kv[GP], vv[GP];
+#pragma unroll
+            for (int pi = 0; pi < GP; ++pi) {
+                const int i = tid + 256 * (g0 + pi), key = kbase + i / (HD / 4), cc = i % (HD / 4);
+                kv[pi] = vv[pi] = make_float4(0, 0, 0, 0);
+                if (key < len) {
+                    kv[pi] = *reinterpret_cast<const float4*>(Kg + (int64_t)key * ld + cc * 4);
+                    vv[pi] = *reinterpret_cast<const float4*>(Vg + (int64_t)key * ld + cc * 4);
+                }
             }
-            *reinterpret_cast<float4*>(&Ks[r * KS + cc * 4]) = kv;
-            *reinterpret_cast<float4*>(&Vs[r * HD + cc * 4]) = vv;
+#pragma unroll
+            for (int pi = 0; pi < GP; ++pi) {
+                const int i = tid + 256 * (g0 + pi), r = i / (HD / 4), cc = i % (HD / 4);
+                *reinterpret_cast<float4*>(&Ks[r * KS + cc * 4]) = kv[pi];
+                *reinterpret_cast<float4*>(&Vs[r * HD + cc * 4]) = vv[pi];
+            }
         }
         __syncthreads();
 
@@ -234,25 +248,38 @@ __global__ __launch_bounds__(256) void attention_bf16_kernel(const uint16_t* __r
     for (int c = 0; c < nchunks; ++c) {
         const int kbase = c * KC;
         __syncthreads();  // previous chunk fully consumed
-        // K rows: 16-byte pieces (8 dims) straight into the padded row layout.
-        constexpr int KP = KC * HD / 8;
-        for (int i = tid; i < KP; i += 256) {
-            const int r = i / (HD / 8), cc = i % (HD / 8);
-            const int key = kbase + r;
-            uint4 kv = make_uint4(0, 0, 0, 0);
-            if (key < len) kv = *reinterpret_cast<const uint4*>(Kg + (int64_t)key * ld + cc * 8);
-            *reinterpret_cast<uint4*>(&Ks[r * KRS + cc * 8]) = kv;
+        // Every K and V load of the chunk is issued before the first LDS
+        // write (one memory round trip per chunk).  K: 16-byte pieces (8
+        // dims) straight into the padded row layout.  V transposed: a thread
+        // takes keys (2p, 2p+1) x 8 dims and writes 8 words Vt[d][2p .. 2p+1].
+        constexpr int KP = KC * HD / 8, KPT = KP / 256;
+        constexpr int VP = (KC / 2) * (HD / 8), VPT = VP / 256;
+        static_assert(KPT * 256 == KP && VPT * 256 == VP, "whole pieces per thread");
+        uint4 kv[KPT], va[VPT], vb2[VPT];
+#pragma unroll
+        for (int pi = 0; pi < KPT; ++pi) {
+            const int i = tid + 256 * pi, key = kbase + i / (HD / 8), cc = i % (HD / 8);
+            kv[pi] = make_uint4(0, 0, 0, 0);
+            if (key < len) kv[pi] = *reinterpret_cast<const uint4*>(Kg + (int64_t)key * ld + cc * 8);
         }
-        // V transposed: a thread takes keys (2p, 2p+1) x 8 dims and writes 8
-        // words Vt[d][2p .. 2p+1].
-        constexpr int VP = (KC / 2) * (HD / 8);
-        for (int i = tid; i < VP; i += 256) {
-            const int pr = i % (KC / 2), cc = i / (KC / 2);
+#pragma unroll
+        for (int pi = 0; pi < VPT; ++pi) {
+            const int i = tid + 256 * pi, pr = i % (KC / 2), cc = i / (KC / 2);
             const int k0 = kbase + 2 * pr;
-            uint4 a = make_uint4(0, 0, 0, 0), bb = make_uint4(0, 0, 0, 0);
-            if (k0 < len) a = *reinterpret_cast<const uint4*>(Vg + (int64_t)k0 * ld + cc * 8);
-            if (k0 + 1 < len) bb = *reinterpret_cast<const uint4*>(Vg + (int64_t)(k0 + 1) * ld + cc * 8);
-            const uint32_t av[4] = {a.x, a.y, a.z, a.w}, bv[4] = {bb.x, bb.y, bb.z, bb.w};
+            va[pi] = vb2[pi] = make_uint4(0, 0, 0, 0);
+            if (k0 < len) va[pi] = *reinterpret_cast<const uint4*>(Vg + (int64_t)k0 * ld + cc * 8);
+            if (k0 + 1 < len) vb2[pi] = *reinterpret_cast<const uint4*>(Vg + (int64_t)(k0 + 1) * ld + cc * 8);
+        }
+#pragma unroll
+        for (int pi = 0; pi < KPT; ++pi) {
+            const int i = tid + 256 * pi, r = i / (HD / 8), cc = i % (HD / 8);
+            *reinterpret_cast<uint4*>(&Ks[r * KRS + cc * 8]) = kv[pi];
+        }
+#pragma unroll
+        for (int pi = 0; pi < VPT; ++pi) {
+            const int i = tid + 256 * pi, pr = i % (KC / 2), cc = i / (KC / 2);
+            const uint32_t av[4] = {va[pi].x, va[pi].y, va[pi].z, va[pi].w};
+            const uint32_t bv[4] = {vb2[pi].x, vb2[pi].y, vb2[pi].z, vb2[pi].w};
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
                 const int d = cc * 8 + 2 * e;
@@ -318,9 +345,10 @@ __global__ __launch_bounds__(256) void attention_bf16_kernel(const uint16_t* __r
             if (kb < nkb) {
 #pragma unroll
                 for (int mm = 0; mm < 2; ++mm) {
-                    v8s_t pa;
-#pragma unroll
-                    for (int e = 0; e < 8; ++e) pa[e] = (short)f32_to_bf16_rne(sc[kb][8 * mm + e]);
+                    const float* pf = reinterpret_cast<const float*>(&sc[kb]) + 8 * mm;
+                    const v8s_t pa = __builtin_bit_cast(
+                        v8s_t, make_uint4(pack_bf16x2(pf[0], pf[1]), pack_bf16x2(pf[2], pf[3]),
+                                          pack_bf16x2(pf[4], pf[5]), pack_bf16x2(pf[6], pf[7])));
                     const int kl = kb * 32 + 16 * mm + 4 * half;   // first of this lane's two 4-key runs
 #pragma unroll
                     for (int j = 0; j < NJ; ++j) {
@@ -351,10 +379,9 @@ __global__ __launch_bounds__(256) void attention_bf16_kernel(const uint16_t* __r
         for (int j = 0; j < NJ; ++j)
 #pragma unroll
             for (int g = 0; g < 4; ++g) {
-                uint2 h;
-                h.x = (uint32_t)f32_to_bf16_rne(o[j][4 * g] * inv) | ((uint32_t)f32_to_bf16_rne(o[j][4 * g + 1] * inv) << 16);
-                h.y = (uint32_t)f32_to_bf16_rne(o[j][4 * g + 2] * inv) | ((uint32_t)f32_to_bf16_rne(o[j][4 * g + 3] * inv) << 16);
-                *reinterpret_cast<uint2*>(dst + j * 32 + 8 * g) = h;
+                *reinterpret_cast<uint2*>(dst + j * 32 + 8 * g) =
+                    make_uint2(pack_bf16x2(o[j][4 * g] * inv, o[j][4 * g + 1] * inv),
+                               pack_bf16x2(o[j][4 * g + 2] * inv, o[j][4 * g + 3] * inv));
             }
     }
 }
