@@ -877,6 +877,124 @@ __global__ __launch_bounds__(256) void gemm_bf16_kernel(GemmArgs p) {
 }
 
 // ---------------------------------------------------------------------------
+// Few-token products (M_max <= 64: a handful of short sentences).  Such a
+// product is a chain of memory round trips rather than MFMA work, so each
+// operand byte is read once and the work is spread over as many workgroups
+// as the shape gives: workgroup (32-column slice, 16-row block, k split s)
+// runs NW waves, wave w taking k in [s*K/S + w*KW, s*K/S + (w+1)*KW), KW =
+// K / (NW*S), with all of a wave's loads in flight at once when KW <=
+// 16*NSTEP.  v_mfma_f32_16x16x4_f32: lane l gives A row l % 16 and W row
+// (output column) l % 16 at k = kb + 4 (l / 16) + e for e = 0..3 of one
+// float4, so A and W pair the same k; each lane then holds rows 4 (l / 16) +
+// i, i = 0..3, of column l % 16.  The wave sums are added through LDS in wave
+// order, then either the bias (+ GELU) is applied (one split), or split s is
+// stored at C + s * split_stride (EPI_NONE: the LayerNorm that follows adds
+// the splits in order).
+// ---------------------------------------------------------------------------
+template <int EPI, int NSTEP, int NW>
+__global__ __launch_bounds__(64 * NW) void gemm_skinny_kernel(GemmArgs p) {
+    typedef float v4f_t __attribute__((ext_vector_type(4)));
+    __shared__ __attribute__((aligned(16))) float red[NW][16][32];
+    const int M = p.M_dev ? *p.M_dev : p.M_max;
+    const int N = p.N, K = p.K;
+    const int S = p.splits > 1 ? p.splits : 1;
+    const int nslices = N / 32;
+    const int blk = blockIdx.x, nb = blk % nslices, m0 = (blk / nslices) * 16, n0 = nb * 32;
+    const int split = blockIdx.y;
+    if (m0 >= M) return;  // uniform over the workgroup
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int r = lane & 15, q = lane >> 4;
+    const int KW = K / (NW * S);
+    const int kb = split * (K / S) + wave * KW + 4 * q;
+    const float* Ar = static_cast<const float*>(p.A) + (int64_t)min(m0 + r, M - 1) * p.lda + kb;
+    const float* W0 = static_cast<const float*>(p.W) + (int64_t)(n0 + r) * p.ldw + kb;
+    const float* W1 = W0 + 16 * p.ldw;
+    v4f_t acc0 = {0.0f, 0.0f, 0.0f, 0.0f}, acc1 = acc0;
+    for (int k = 0; k < KW; k += 16 * NSTEP) {
+        float4 a[NSTEP], w0[NSTEP], w1[NSTEP];
+#pragma unroll
+        for (int j = 0; j < NSTEP; ++j) {
+            a[j] = *reinterpret_cast<const float4*>(Ar + k + 16 * j);
+            w0[j] = *reinterpret_cast<const float4*>(W0 + k + 16 * j);
+            w1[j] = *reinterpret_cast<const float4*>(W1 + k + 16 * j);
+        }
+#pragma unroll
+        for (int j = 0; j < NSTEP; ++j) {
+            const float av[4] = {a[j].x, a[j].y, a[j].z, a[j].w};
+            const float b0[4] = {w0[j].x, w0[j].y, w0[j].z, w0[j].w};
+            const float b1[4] = {w1[j].x, w1[j].y, w1[j].z, w1[j].w};
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                acc0 = __builtin_amdgcn_mfma_f32_16x16x4f32(av[e], b0[e], acc0, 0, 0, 0);
+                acc1 = __builtin_amdgcn_mfma_f32_16x16x4f32(av[e], b1[e], acc1, 0, 0, 0);
+            }
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        red[wave][4 * q + i][r] = acc0[i];
+        red[wave][4 * q + i][16 + r] = acc1[i];
+    }
+    __syncthreads();
+    // Element pairs e = t, t + 64 NW, ... of the 16 x 32 block: row e / 16,
+    // columns 2 (e % 16) .. +1.
+    for (int e = tid; e < 256; e += 64 * NW) {
+        const int row = e >> 4, col = 2 * (e & 15);
+        const int grow = m0 + row, gcol = n0 + col;
+        if (grow >= M) continue;
+        float2 v = *reinterpret_cast<const float2*>(&red[0][row][col]);
+#pragma unroll
+        for (int w = 1; w < NW; ++w) {
+            const float2 pw = *reinterpret_cast<const float2*>(&red[w][row][col]);
+            v.x += pw.x;
+            v.y += pw.y;
+        }
+        if constexpr (EPI != EPI_NONE) {
+            const float2 b2 = *reinterpret_cast<const float2*>(p.bias + gcol);
+            v.x += b2.x;
+            v.y += b2.y;
+            if constexpr (EPI == EPI_BIAS_GELU) {
+                v.x = gelu_tanh_fast(v.x);
+                v.y = gelu_tanh_fast(v.y);
+            }
+        }
+        *reinterpret_cast<float2*>(p.C + split * p.split_stride + (int64_t)grow * p.ldc + gcol) = v;
+    }
+}
+
+bool gemm_f32_skinny_fits(int M_max, int N, int K) {
+    return M_max > 0 && M_max <= SKINNY_MAX_ROWS && N % 32 == 0 && K % 64 == 0 && K > 0;
+}
+
+template <int EPI, int NW>
+static hipError_t launch_skinny_nw(const GemmArgs& a, hipStream_t s) {
+    const int S = a.splits > 1 ? a.splits : 1;
+    const int steps = a.K / (16 * NW * S);        // 16-deep steps per wave
+    const dim3 grid((a.N / 32) * ((a.M_max + 15) / 16), S), block(64 * NW);
+    if (steps % 4 == 0) hipLaunchKernelGGL((gemm_skinny_kernel<EPI, 4, NW>), grid, block, 0, s, a);
+    else if (steps % 3 == 0) hipLaunchKernelGGL((gemm_skinny_kernel<EPI, 3, NW>), grid, block, 0, s, a);
+    else if (steps % 2 == 0) hipLaunchKernelGGL((gemm_skinny_kernel<EPI, 2, NW>), grid, block, 0, s, a);
+    else hipLaunchKernelGGL((gemm_skinny_kernel<EPI, 1, NW>), grid, block, 0, s, a);
+    return hipGetLastError();
+}
+
+// 8 waves when each still gets a whole 16-deep step, else 4 (K % (64 S) == 0).
+template <int EPI>
+static hipError_t launch_skinny_epi(const GemmArgs& a, hipStream_t s) {
+    const int S = a.splits > 1 ? a.splits : 1;
+    return a.K % (128 * S) == 0 ? launch_skinny_nw<EPI, 8>(a, s) : launch_skinny_nw<EPI, 4>(a, s);
+}
+
+static hipError_t launch_skinny(const GemmArgs& a, int epi, hipStream_t s) {
+    switch (epi) {
+        case EPI_BIAS: return launch_skinny_epi<EPI_BIAS>(a, s);
+        case EPI_BIAS_GELU: return launch_skinny_epi<EPI_BIAS_GELU>(a, s);
+        case EPI_NONE: return launch_skinny_epi<EPI_NONE>(a, s);
+        default: return hipErrorInvalidValue;
+    }
+}
+
+// ---------------------------------------------------------------------------
 // launchers
 // ---------------------------------------------------------------------------
 template <int BM, int BN, int BK, int WAVES_M, int WAVES_N, bool BF16, bool KFULL = false>
@@ -975,6 +1093,10 @@ hipError_t launch_gemm_f32(const GemmArgs& a, int epi, hipStream_t s) {
     //    item of its own, written to its own partial output; mid-size split
     //    products run 128 x 128 x 32 tiles, two workgroups per CU.
     const int S = a.splits > 1 ? a.splits : 1;
+    //  * at most 64 rows: the few-token kernel (gemm_skinny_kernel); bias-free
+    //    products split over K as below.
+    if (ok && gemm_f32_skinny_fits(a.M_max, a.N, a.K) && a.K % (64 * S) == 0 && (S == 1 || epi == EPI_NONE))
+        return launch_skinny(a, epi, s);
     if (S > 1 && (epi != EPI_NONE || !ok || a.K % (32 * S))) return hipErrorInvalidValue;
     const int64_t tiles128 = (int64_t)((a.M_max + 127) / 128) * ((a.N + 127) / 128);
     if (ok && a.K % (64 * S) == 0 && 2 * tiles128 < (int64_t)cu_count())

@@ -31,6 +31,11 @@ struct GemmArgs {
     float ln_eps;
 };
 
+// The few-token GEMM path: M_max <= SKINNY_MAX_ROWS rows in 16-row blocks,
+// N % 32 == 0, K % 64 == 0, 16-byte aligned rows and operands.
+constexpr int SKINNY_MAX_ROWS = 64;
+bool gemm_f32_skinny_fits(int M_max, int N, int K);
+
 // Compute units of the current device (queried once).
 int device_cu_count();
 

@@ -231,6 +231,14 @@ __device__ __forceinline__ float group_sum(float v) {
 template <int NV, int LPR>
 __device__ __forceinline__ void ln_row4(float4 (&v)[NV], int sub, int H, const float* g,
                                         const float* b, float eps, float* y, uint16_t* y16) {
+    // gamma / beta are loaded first, so their memory round trip overlaps the
+    // row reductions instead of following them.
+    float4 g4[NV], b4[NV];
+#pragma unroll
+    for (int c = 0; c < NV; ++c) {
+        g4[c] = *reinterpret_cast<const float4*>(g + 4 * (c * LPR + sub));
+        b4[c] = *reinterpret_cast<const float4*>(b + 4 * (c * LPR + sub));
+    }
     float s = 0.0f;
 #pragma unroll
     for (int c = 0; c < NV; ++c) s += (v[c].x + v[c].y) + (v[c].z + v[c].w);
@@ -246,13 +254,11 @@ __device__ __forceinline__ void ln_row4(float4 (&v)[NV], int sub, int H, const f
 #pragma unroll
     for (int c = 0; c < NV; ++c) {
         const int i = 4 * (c * LPR + sub);
-        const float4 g4 = *reinterpret_cast<const float4*>(g + i);
-        const float4 b4 = *reinterpret_cast<const float4*>(b + i);
         float4 o;
-        o.x = (v[c].x - mean) * inv_std * g4.x + b4.x;
-        o.y = (v[c].y - mean) * inv_std * g4.y + b4.y;
-        o.z = (v[c].z - mean) * inv_std * g4.z + b4.z;
-        o.w = (v[c].w - mean) * inv_std * g4.w + b4.w;
+        o.x = (v[c].x - mean) * inv_std * g4[c].x + b4[c].x;
+        o.y = (v[c].y - mean) * inv_std * g4[c].y + b4[c].y;
+        o.z = (v[c].z - mean) * inv_std * g4[c].z + b4[c].z;
+        o.w = (v[c].w - mean) * inv_std * g4[c].w + b4[c].w;
         *reinterpret_cast<float4*>(y + i) = o;
         if (y16) {
             uint2 h;
@@ -263,35 +269,71 @@ __device__ __forceinline__ void ln_row4(float4 (&v)[NV], int sub, int H, const f
     }
 }
 
-template <int NV, int LPR>
-__global__ __launch_bounds__(256) void add_layernorm4_kernel(const float* __restrict__ y,
-                                                             const float* __restrict__ bias,
-                                                             float* x, const float* __restrict__ g,
-                                                             const float* __restrict__ bta,
-                                                             int rows_max, const int* rows_dev,
-                                                             int H, float eps, uint16_t* x16,
-                                                             int nparts, int64_t part_stride) {
+// x = LayerNorm((y + bias) + x) on float4 rows.  PB == 0: y is one product;
+// otherwise y holds nparts split-K partials part_stride floats apart, added in
+// order, with their loads going out PB partials at a time (an index past the
+// last partial re-reads the last one and is not added), so a row waits for
+// one memory round trip per PB partials rather than one per partial.
+template <int NV, int LPR, int PB>
+__device__ __forceinline__ void add_layernorm4_row(const float* __restrict__ y, const float* __restrict__ bias,
+                                                   float* x, const float* __restrict__ g,
+                                                   const float* __restrict__ bta, int rows_max,
+                                                   const int* rows_dev, int H, float eps, uint16_t* x16,
+                                                   int nparts, int64_t part_stride) {
     constexpr int RPB = 256 / LPR;                // rows per workgroup
     const int row = blockIdx.x * RPB + threadIdx.x / LPR, sub = threadIdx.x % LPR;
     const int rows = rows_dev ? *rows_dev : rows_max;
     if (row >= rows) return;
     const float* yr = y + (int64_t)row * H;
     float* xr = x + (int64_t)row * H;
-    float4 v[NV];
+    float4 a[NV], bb[NV], r[NV];
 #pragma unroll
     for (int c = 0; c < NV; ++c) {
         const int i = 4 * (c * LPR + sub);
-        float4 a = *reinterpret_cast<const float4*>(yr + i);
-        for (int q = 1; q < nparts; ++q) {        // split-K partials, in order
-            const float4 pq = *reinterpret_cast<const float4*>(yr + q * part_stride + i);
-            a.x += pq.x; a.y += pq.y; a.z += pq.z; a.w += pq.w;
-        }
-        const float4 bb = *reinterpret_cast<const float4*>(bias + i);
-        const float4 r = *reinterpret_cast<const float4*>(xr + i);
-        v[c] = make_float4((a.x + bb.x) + r.x, (a.y + bb.y) + r.y, (a.z + bb.z) + r.z, (a.w + bb.w) + r.w);
+        a[c] = *reinterpret_cast<const float4*>(yr + i);
+        bb[c] = *reinterpret_cast<const float4*>(bias + i);
+        r[c] = *reinterpret_cast<const float4*>(xr + i);
     }
+    if constexpr (PB > 0) {
+        for (int q0 = 1; q0 < nparts; q0 += PB) {
+            float4 pq[PB][NV];
+#pragma unroll
+            for (int k = 0; k < PB; ++k) {
+                const float* pr = yr + (int64_t)min(q0 + k, nparts - 1) * part_stride;
+#pragma unroll
+                for (int c = 0; c < NV; ++c) pq[k][c] = *reinterpret_cast<const float4*>(pr + 4 * (c * LPR + sub));
+            }
+#pragma unroll
+            for (int k = 0; k < PB; ++k)
+                if (q0 + k < nparts) {
+#pragma unroll
+                    for (int c = 0; c < NV; ++c) {
+                        a[c].x += pq[k][c].x; a[c].y += pq[k][c].y; a[c].z += pq[k][c].z; a[c].w += pq[k][c].w;
+                    }
+                }
+        }
+    }
+    float4 v[NV];
+#pragma unroll
+    for (int c = 0; c < NV; ++c)
+        v[c] = make_float4((a[c].x + bb[c].x) + r[c].x, (a[c].y + bb[c].y) + r[c].y,
+                           (a[c].z + bb[c].z) + r[c].z, (a[c].w + bb[c].w) + r[c].w);
     ln_row4<NV, LPR>(v, sub, H, g, bta, eps, xr, x16 ? x16 + (int64_t)row * H : nullptr);
 }
+
+#define EBH_ADD_LN4_KERNEL(NAME, PB)                                                                    \
+    template <int NV, int LPR>                                                                          \
+    __global__ __launch_bounds__(256) void NAME(const float* __restrict__ y, const float* __restrict__ bias, \
+                                                float* x, const float* __restrict__ g,                  \
+                                                const float* __restrict__ bta, int rows_max,            \
+                                                const int* rows_dev, int H, float eps, uint16_t* x16,   \
+                                                int nparts, int64_t part_stride) {                      \
+        add_layernorm4_row<NV, LPR, PB>(y, bias, x, g, bta, rows_max, rows_dev, H, eps, x16, nparts,    \
+                                        part_stride);                                                   \
+    }
+EBH_ADD_LN4_KERNEL(add_layernorm4_kernel, 0)       // one product
+EBH_ADD_LN4_KERNEL(add_layernorm4_p4_kernel, 4)    // split-K partials
+#undef EBH_ADD_LN4_KERNEL
 
 // The same with the projection y stored as bf16 (bf16 models write the
 // attention-output and FFN-down products in bf16); the sum, statistics and
@@ -423,8 +465,12 @@ hipError_t launch_add_layernorm(const float* y, const float* bias, float* x, con
     row4_shape(H, lpr, nv);
     if (lpr && al16(y) && al16(bias) && al16(x) && al16(g) && al16(b) && (!x16 || ((uintptr_t)x16 & 7) == 0) &&
         part_stride % 4 == 0) {
-        EBH_ROW4_DISPATCH(add_layernorm4_kernel, lpr, nv, rows_max, s, y, bias, x, g, b, rows_max,
-                          rows_dev, H, eps, x16, nparts, part_stride);
+        if (nparts > 1)
+            EBH_ROW4_DISPATCH(add_layernorm4_p4_kernel, lpr, nv, rows_max, s, y, bias, x, g, b, rows_max,
+                              rows_dev, H, eps, x16, nparts, part_stride);
+        else
+            EBH_ROW4_DISPATCH(add_layernorm4_kernel, lpr, nv, rows_max, s, y, bias, x, g, b, rows_max,
+                              rows_dev, H, eps, x16, nparts, part_stride);
         return hipGetLastError();
     }
     const dim3 grid((rows_max + 3) / 4);

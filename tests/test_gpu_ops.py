@@ -110,6 +110,33 @@ def test_gemm_f32_dispatch_paths(env, M, N, K, epi):
     np.testing.assert_allclose(dC.cpu().numpy(), want, rtol=0, atol=tol)
 
 
+@pytest.mark.parametrize("M,N,K", [(1, 32, 64), (16, 1152, 384), (33, 384, 1536), (64, 3072, 768),
+                                   (50, 96, 192), (7, 64, 320)])
+@pytest.mark.parametrize("epi", [0, 1, 3])
+def test_gemm_f32_few_tokens(env, M, N, K, epi):
+    """At most 64 rows: the few-token kernel (4 or 8 waves, 1 to 4 16-deep
+    steps per load batch, 1 to 4 row blocks with a ragged last one, a row
+    stride above K) against the float64 product."""
+    torch, eb, Nn, L = env
+    rng = np.random.default_rng(3 * M + N + K + epi)
+    lda = K + 4
+    A = rng.standard_normal((M, lda)).astype(np.float32)
+    W = (0.05 * rng.standard_normal((N, K))).astype(np.float32)
+    bias = rng.standard_normal(N).astype(np.float32)
+    dA, dW, db = dev(torch, A), dev(torch, W), dev(torch, bias)
+    dC = torch.full((M + 3, N), float("nan"), device="cuda")
+    Nn.check(L.ebh_op_gemm(vp(dA), lda, vp(dW), K, Nn.EBH_DTYPE_F32, vp(db) if epi != 3 else None,
+                           None, N, vp(dC), N, M, N, K, epi, stream(torch)))
+    torch.cuda.synchronize()
+    want = A[:, :K].astype(np.float64) @ W.T.astype(np.float64) + (bias if epi != 3 else 0.0)
+    if epi == 1:
+        want = gelu64(want)
+    got = dC.cpu().numpy()
+    assert np.isnan(got[M:]).all(), "rows past M were written"
+    tol = 2e-6 * np.sqrt(K) * (np.abs(A[:, :K]).max() * np.abs(W).max() * np.sqrt(K)) + 1e-5
+    np.testing.assert_allclose(got[:M], want, rtol=0, atol=tol)
+
+
 def _bf16_round(x):
     import torch
     return torch.from_numpy(np.ascontiguousarray(x, np.float32)).to(torch.bfloat16).float().numpy()
