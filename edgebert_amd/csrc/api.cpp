@@ -10,6 +10,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <atomic>
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
@@ -94,6 +95,21 @@ struct GraphEntry {
 };
 constexpr size_t MAX_GRAPHS = 16;
 
+// Pinned host staging of the blocking entry points.  There are two sets, so a
+// caller's forward can be enqueued behind another caller's while that one
+// still runs or is being copied out.  A caller holds its slot from staging to
+// copy-out, and the model's lock only while it stages and enqueues.
+struct HostSlot {
+    int* ids = nullptr;
+    int* mask = nullptr;
+    float* out = nullptr;
+    int* err = nullptr;
+    int64_t cap = 0, out_cap = 0;
+    hipEvent_t done = nullptr;  // completion of this slot's last forward
+    std::mutex mu;
+};
+constexpr int N_HOST_SLOTS = 2;
+
 }  // namespace
 
 struct ebh_model {
@@ -114,12 +130,9 @@ struct ebh_model {
     bool has_done = false;
     Workspace ws;
     int last_B = 0;
-    // pinned host staging for the blocking API
-    int* h_ids = nullptr;
-    int* h_mask = nullptr;
-    float* h_out = nullptr;
-    int* h_err = nullptr;
-    int64_t h_cap = 0, h_out_cap = 0;
+    // pinned host staging for the blocking API, taken round robin
+    HostSlot slots[N_HOST_SLOTS];
+    std::atomic<unsigned> slot_rr{0};
     // recorded forwards (GraphEntry), least recently used dropped first
     std::vector<GraphEntry> graphs;
     uint64_t graph_clock = 0;
@@ -280,29 +293,32 @@ int ensure_workspace(ebh_model* m, int B, int S) {
     return EBH_OK;
 }
 
-int ensure_host_staging(ebh_model* m, int64_t T, int64_t outn) {
-    if (T > m->h_cap || outn > m->h_out_cap) {
+// Called with the model's lock and the slot's lock held (so the slot's last
+// forward has completed).
+int ensure_host_staging(ebh_model* m, HostSlot& hs, int64_t T, int64_t outn) {
+    if (T > hs.cap || outn > hs.out_cap) {
         // Recorded host-path forwards copy from / to these buffers.
         if (m->has_done) HIP_TRY(hipEventSynchronize(m->done));
         drop_graphs(m);
     }
-    if (T > m->h_cap) {
-        if (m->h_ids) (void)hipHostFree(m->h_ids);
-        if (m->h_mask) (void)hipHostFree(m->h_mask);
-        m->h_ids = m->h_mask = nullptr;
-        m->h_cap = 0;
-        HIP_TRY(hipHostMalloc((void**)&m->h_ids, std::max<int64_t>(T, 1) * 4, hipHostMallocDefault));
-        HIP_TRY(hipHostMalloc((void**)&m->h_mask, std::max<int64_t>(T, 1) * 4, hipHostMallocDefault));
-        m->h_cap = T;
+    if (T > hs.cap) {
+        if (hs.ids) (void)hipHostFree(hs.ids);
+        if (hs.mask) (void)hipHostFree(hs.mask);
+        hs.ids = hs.mask = nullptr;
+        hs.cap = 0;
+        HIP_TRY(hipHostMalloc((void**)&hs.ids, std::max<int64_t>(T, 1) * 4, hipHostMallocDefault));
+        HIP_TRY(hipHostMalloc((void**)&hs.mask, std::max<int64_t>(T, 1) * 4, hipHostMallocDefault));
+        hs.cap = T;
     }
-    if (outn > m->h_out_cap) {
-        if (m->h_out) (void)hipHostFree(m->h_out);
-        m->h_out = nullptr;
-        m->h_out_cap = 0;
-        HIP_TRY(hipHostMalloc((void**)&m->h_out, std::max<int64_t>(outn, 1) * 4, hipHostMallocDefault));
-        m->h_out_cap = outn;
+    if (outn > hs.out_cap) {
+        if (hs.out) (void)hipHostFree(hs.out);
+        hs.out = nullptr;
+        hs.out_cap = 0;
+        HIP_TRY(hipHostMalloc((void**)&hs.out, std::max<int64_t>(outn, 1) * 4, hipHostMallocDefault));
+        hs.out_cap = outn;
     }
-    if (!m->h_err) HIP_TRY(hipHostMalloc((void**)&m->h_err, 4, hipHostMallocDefault));
+    if (!hs.err) HIP_TRY(hipHostMalloc((void**)&hs.err, 4, hipHostMallocDefault));
+    if (!hs.done) HIP_TRY(hipEventCreateWithFlags(&hs.done, hipEventDisableTiming));
     return EBH_OK;
 }
 
@@ -506,29 +522,35 @@ hipGraphExec_t graph_for(ebh_model* m, const GraphEntry& key, hipStream_t s, Bod
     return e->exec;
 }
 
-// One forward on stream s, ordered after the model's previous work.  host:
-// ids / mask come from the pinned staging buffers and the result (d_scores
-// if given, else d_out) and the id-range flag go back to them.
+// One forward on stream s, ordered after the model's previous work.  hs (the
+// blocking entry points): ids / mask come from that slot's pinned staging
+// buffers, and the result (d_scores if given, else d_out) and the id-range
+// flag go back to it.
 int run_forward(ebh_model* m, const int* d_ids, const int* d_mask, int B, int S, int normalize,
-                float* d_out, hipStream_t s, float* d_scores, bool host) {
+                float* d_out, hipStream_t s, float* d_scores, HostSlot* hs) {
+    const bool host = hs != nullptr;
     Workspace& w = m->ws;
     const int64_t T = (int64_t)B * S;
     const size_t n_out = d_scores ? (size_t)B : (size_t)B * m->cfg.hidden_size;
     if (m->has_done) HIP_TRY(hipStreamWaitEvent(s, m->done, 0));
     auto body = [&](hipStream_t st) -> int {
         if (host) {
-            HIP_TRY(hipMemcpyAsync(w.ids, m->h_ids, T * 4, hipMemcpyHostToDevice, st));
-            HIP_TRY(hipMemcpyAsync(w.mask, m->h_mask, T * 4, hipMemcpyHostToDevice, st));
+            HIP_TRY(hipMemcpyAsync(w.ids, hs->ids, T * 4, hipMemcpyHostToDevice, st));
+            HIP_TRY(hipMemcpyAsync(w.mask, hs->mask, T * 4, hipMemcpyHostToDevice, st));
         }
         int rc = enqueue_kernels(m, d_ids, d_mask, B, S, normalize, d_out, st, d_scores);
         if (rc) return rc;
         if (host) {
-            HIP_TRY(hipMemcpyAsync(m->h_out, d_scores ? d_scores : d_out, n_out * 4, hipMemcpyDeviceToHost, st));
-            HIP_TRY(hipMemcpyAsync(m->h_err, w.err, 4, hipMemcpyDeviceToHost, st));
+            HIP_TRY(hipMemcpyAsync(hs->out, d_scores ? d_scores : d_out, n_out * 4, hipMemcpyDeviceToHost, st));
+            HIP_TRY(hipMemcpyAsync(hs->err, w.err, 4, hipMemcpyDeviceToHost, st));
         }
         return EBH_OK;
     };
-    const GraphEntry key{B, S, normalize, host ? 1 : 0, d_ids, d_mask, d_out, d_scores, 0, nullptr, 0};
+    // Host-path recordings bake in the slot's staging buffers, so each slot
+    // has its own.
+    const GraphEntry key{B, S, normalize, host ? 1 : 0, host ? (const void*)hs->ids : d_ids,
+                         host ? (const void*)hs->mask : d_mask, host ? (void*)hs->out : d_out, d_scores,
+                         0, nullptr, 0};
     if (hipGraphExec_t exec = graph_for(m, key, s, body)) {
         HIP_TRY(hipGraphLaunch(exec, s));
     } else {
@@ -536,26 +558,38 @@ int run_forward(ebh_model* m, const int* d_ids, const int* d_mask, int B, int S,
         if (rc) return rc;
     }
     HIP_TRY(hipEventRecord(m->done, s));
+    if (hs) HIP_TRY(hipEventRecord(hs->done, s));
     m->has_done = true;
     m->last_B = B;
     return EBH_OK;
 }
 
-// Blocking forward from int32 host ids/mask already validated into h_ids/h_mask.
-// Staged host ids / mask -> device forward -> out ([B, H], or the [B]
-// cross-encoder scores when `score`).
-int forward_host_staged(ebh_model* m, int B, int S, int normalize, float* out, bool score = false) {
+// Blocking forward from host buffers.  `stage(ids, mask)` writes (and
+// validates) the caller's ids / mask into a slot's pinned buffers; the forward
+// is enqueued under the model's lock, which is released before the wait, so
+// the next caller's forward can be queued behind this one while it runs.
+// The result ([B, H] vectors, or [B] scores) is copied to out.
+template <class Stage>
+int host_forward(ebh_model* m, int B, int S, int normalize, float* out, bool score, Stage&& stage) {
     const int H = m->cfg.hidden_size;
+    const int64_t T = (int64_t)B * S;
     const size_t n_out = score ? (size_t)B : (size_t)B * H;
-    hipStream_t s = m->stream;
-    int rc = ensure_workspace(m, B, S);
-    if (rc) return rc;
-    if ((rc = run_forward(m, m->ws.ids, m->ws.mask, B, S, normalize, m->ws.out, s,
-                          score ? m->ws.scores : nullptr, true)))
-        return rc;
-    HIP_TRY(hipStreamSynchronize(s));
-    if (*m->h_err) return fail(EBH_ERR_RANGE, "token id out of range for vocab %d", m->cfg.vocab_size);
-    memcpy(out, m->h_out, n_out * 4);
+    HostSlot& hs = m->slots[m->slot_rr.fetch_add(1) % N_HOST_SLOTS];
+    std::lock_guard<std::mutex> slot_lock(hs.mu);
+    {
+        std::lock_guard<std::mutex> lk(m->mu);
+        HIP_TRY(hipSetDevice(m->device));
+        int rc = ensure_host_staging(m, hs, T, (int64_t)B * H);
+        if (rc) return rc;
+        if ((rc = stage(hs.ids, hs.mask))) return rc;
+        if ((rc = ensure_workspace(m, B, S))) return rc;
+        if ((rc = run_forward(m, m->ws.ids, m->ws.mask, B, S, normalize, m->ws.out, m->stream,
+                              score ? m->ws.scores : nullptr, &hs)))
+            return rc;
+    }
+    HIP_TRY(hipEventSynchronize(hs.done));
+    if (*hs.err) return fail(EBH_ERR_RANGE, "token id out of range for vocab %d", m->cfg.vocab_size);
+    memcpy(out, hs.out, n_out * 4);
     return EBH_OK;
 }
 
@@ -772,10 +806,13 @@ void ebh_destroy(ebh_model* m) {
         drop_graphs(m);
         if (m->ws.base) (void)hipFree(m->ws.base);
         if (m->wbase) (void)hipFree(m->wbase);
-        if (m->h_ids) (void)hipHostFree(m->h_ids);
-        if (m->h_mask) (void)hipHostFree(m->h_mask);
-        if (m->h_out) (void)hipHostFree(m->h_out);
-        if (m->h_err) (void)hipHostFree(m->h_err);
+        for (HostSlot& hs : m->slots) {
+            if (hs.ids) (void)hipHostFree(hs.ids);
+            if (hs.mask) (void)hipHostFree(hs.mask);
+            if (hs.out) (void)hipHostFree(hs.out);
+            if (hs.err) (void)hipHostFree(hs.err);
+            if (hs.done) (void)hipEventDestroy(hs.done);
+        }
         if (m->done) (void)hipEventDestroy(m->done);
         if (m->stream) (void)hipStreamDestroy(m->stream);
     }
@@ -794,25 +831,40 @@ int ebh_forward(ebh_model* m, const float* input_ids, const float* attention_mas
         memset(out, 0, sizeof(float) * (size_t)B * H);
         return EBH_OK;
     }
-    std::lock_guard<std::mutex> lk(m->mu);
-    HIP_TRY(hipSetDevice(m->device));
     const int64_t T = (int64_t)B * S;
-    if ((rc = ensure_host_staging(m, T, (int64_t)B * H))) return rc;
+    return host_forward(m, B, S, 0, out, false, [&](int* h_ids, int* h_mask) -> int {
+        for (int64_t i = 0; i < T; ++i) {
+            // `token_id as usize` (src/lib.rs:639): truncation; NaN / negatives -> 0.
+            const float f = input_ids[i];
+            int64_t id = (f > 0.0f) ? (f >= 9.2e18f ? INT64_MAX : (int64_t)f) : 0;
+            if (id >= m->cfg.vocab_size)
+                return fail(EBH_ERR_RANGE, "token id %lld at [%lld, %lld] out of range for vocab %d",
+                            (long long)id, (long long)(i / S), (long long)(i % S), m->cfg.vocab_size);
+            const float mk = attention_mask[i];
+            if (mk != 0.0f && mk != 1.0f)
+                return fail(EBH_ERR_INVALID_ARG, "attention mask value %g at [%lld, %lld] is not 0 or 1",
+                            (double)mk, (long long)(i / S), (long long)(i % S));
+            h_ids[i] = (int)id;
+            h_mask[i] = mk != 0.0f;
+        }
+        return EBH_OK;
+    });
+}
+
+// u32 ids / mask (the tokenizer's output) -> pinned staging, validated.
+static int stage_u32(const ebh_model* m, const uint32_t* ids, const uint32_t* mask, int S, int64_t T, int* h_ids,
+              int* h_mask) {
     for (int64_t i = 0; i < T; ++i) {
-        // `token_id as usize` (src/lib.rs:639): truncation; NaN / negatives -> 0.
-        const float f = input_ids[i];
-        int64_t id = (f > 0.0f) ? (f >= 9.2e18f ? INT64_MAX : (int64_t)f) : 0;
-        if (id >= m->cfg.vocab_size)
-            return fail(EBH_ERR_RANGE, "token id %lld at [%lld, %lld] out of range for vocab %d",
-                        (long long)id, (long long)(i / S), (long long)(i % S), m->cfg.vocab_size);
-        const float mk = attention_mask[i];
-        if (mk != 0.0f && mk != 1.0f)
-            return fail(EBH_ERR_INVALID_ARG, "attention mask value %g at [%lld, %lld] is not 0 or 1",
-                        (double)mk, (long long)(i / S), (long long)(i % S));
-        m->h_ids[i] = (int)id;
-        m->h_mask[i] = mk != 0.0f;
+        if (ids[i] >= (uint32_t)m->cfg.vocab_size)
+            return fail(EBH_ERR_RANGE, "token id %u at [%lld, %lld] out of range for vocab %d",
+                        ids[i], (long long)(i / S), (long long)(i % S), m->cfg.vocab_size);
+        if (mask[i] > 1)
+            return fail(EBH_ERR_INVALID_ARG, "attention mask value %u at [%lld, %lld] is not 0 or 1",
+                        mask[i], (long long)(i / S), (long long)(i % S));
+        h_ids[i] = (int)ids[i];
+        h_mask[i] = (int)mask[i];
     }
-    return forward_host_staged(m, B, S, 0, out);
+    return EBH_OK;
 }
 
 int ebh_encode(ebh_model* m, const uint32_t* ids, const uint32_t* mask, int32_t B, int32_t S,
@@ -827,21 +879,10 @@ int ebh_encode(ebh_model* m, const uint32_t* ids, const uint32_t* mask, int32_t 
         memset(out, 0, sizeof(float) * (size_t)B * H);
         return EBH_OK;
     }
-    std::lock_guard<std::mutex> lk(m->mu);
-    HIP_TRY(hipSetDevice(m->device));
     const int64_t T = (int64_t)B * S;
-    if ((rc = ensure_host_staging(m, T, (int64_t)B * H))) return rc;
-    for (int64_t i = 0; i < T; ++i) {
-        if (ids[i] >= (uint32_t)m->cfg.vocab_size)
-            return fail(EBH_ERR_RANGE, "token id %u at [%lld, %lld] out of range for vocab %d",
-                        ids[i], (long long)(i / S), (long long)(i % S), m->cfg.vocab_size);
-        if (mask[i] > 1)
-            return fail(EBH_ERR_INVALID_ARG, "attention mask value %u at [%lld, %lld] is not 0 or 1",
-                        mask[i], (long long)(i / S), (long long)(i % S));
-        m->h_ids[i] = (int)ids[i];
-        m->h_mask[i] = (int)mask[i];
-    }
-    return forward_host_staged(m, B, S, normalize ? 1 : 0, out);
+    return host_forward(m, B, S, normalize ? 1 : 0, out, false, [&](int* h_ids, int* h_mask) {
+        return stage_u32(m, ids, mask, S, T, h_ids, h_mask);
+    });
 }
 
 int ebh_encode_device(ebh_model* m, const int32_t* ids, const int32_t* mask, int32_t B,
@@ -860,7 +901,7 @@ int ebh_encode_device(ebh_model* m, const int32_t* ids, const int32_t* mask, int
         return EBH_OK;
     }
     if ((rc = ensure_workspace(m, B, S))) return rc;
-    return run_forward(m, ids, mask, B, S, normalize ? 1 : 0, out, s, nullptr, false);
+    return run_forward(m, ids, mask, B, S, normalize ? 1 : 0, out, s, nullptr, nullptr);
 }
 
 int ebh_score(ebh_model* m, const uint32_t* ids, const uint32_t* mask, int32_t B, int32_t S,
@@ -872,21 +913,10 @@ int ebh_score(ebh_model* m, const uint32_t* ids, const uint32_t* mask, int32_t B
     if (B == 0) return EBH_OK;
     if (!ids || !mask || !scores) return fail(EBH_ERR_INVALID_ARG, "null buffer");
     if (S == 0) return fail(EBH_ERR_INVALID_ARG, "empty pair encoding (S == 0)");
-    std::lock_guard<std::mutex> lk(m->mu);
-    HIP_TRY(hipSetDevice(m->device));
     const int64_t T = (int64_t)B * S;
-    if ((rc = ensure_host_staging(m, T, (int64_t)B * m->cfg.hidden_size))) return rc;
-    for (int64_t i = 0; i < T; ++i) {
-        if (ids[i] >= (uint32_t)m->cfg.vocab_size)
-            return fail(EBH_ERR_RANGE, "token id %u at [%lld, %lld] out of range for vocab %d",
-                        ids[i], (long long)(i / S), (long long)(i % S), m->cfg.vocab_size);
-        if (mask[i] > 1)
-            return fail(EBH_ERR_INVALID_ARG, "attention mask value %u at [%lld, %lld] is not 0 or 1",
-                        mask[i], (long long)(i / S), (long long)(i % S));
-        m->h_ids[i] = (int)ids[i];
-        m->h_mask[i] = (int)mask[i];
-    }
-    return forward_host_staged(m, B, S, 0, scores, true);
+    return host_forward(m, B, S, 0, scores, true, [&](int* h_ids, int* h_mask) {
+        return stage_u32(m, ids, mask, S, T, h_ids, h_mask);
+    });
 }
 
 // Tokenised texts (host threads, outside the model's lock) -> pinned staging -> forward.
@@ -903,17 +933,15 @@ static int forward_texts(ebh_model* m, const ebh_tokenizer* t, const char* const
     int S = 0;
     if ((rc = ebh::tokenize_batch(t, texts, lens, n, nthreads, seqs, &S))) return rc;
     if ((rc = check_dims(m, n, S))) return rc;
-    const int H = m->cfg.hidden_size;
-    std::lock_guard<std::mutex> lk(m->mu);
-    HIP_TRY(hipSetDevice(m->device));
     const int64_t T = (int64_t)n * S;
-    if ((rc = ensure_host_staging(m, T, (int64_t)n * H))) return rc;
-    ebh::write_padded(t, seqs, S, m->h_ids, m->h_mask);
-    for (int64_t i = 0; i < T; ++i)
-        if (m->h_ids[i] < 0 || m->h_ids[i] >= m->cfg.vocab_size)
-            return fail(EBH_ERR_RANGE, "token id %d at [%lld, %lld] out of range for vocab %d", m->h_ids[i],
-                        (long long)(i / S), (long long)(i % S), m->cfg.vocab_size);
-    return forward_host_staged(m, n, S, normalize ? 1 : 0, out, score);
+    return host_forward(m, n, S, normalize ? 1 : 0, out, score, [&](int* h_ids, int* h_mask) -> int {
+        ebh::write_padded(t, seqs, S, h_ids, h_mask);
+        for (int64_t i = 0; i < T; ++i)
+            if (h_ids[i] < 0 || h_ids[i] >= m->cfg.vocab_size)
+                return fail(EBH_ERR_RANGE, "token id %d at [%lld, %lld] out of range for vocab %d", h_ids[i],
+                            (long long)(i / S), (long long)(i % S), m->cfg.vocab_size);
+        return EBH_OK;
+    });
 }
 
 int ebh_encode_texts(ebh_model* m, const ebh_tokenizer* t, const char* const* texts, const int64_t* lens,
@@ -955,7 +983,7 @@ int ebh_score_device(ebh_model* m, const int32_t* ids, const int32_t* mask, int3
     HIP_TRY(hipSetDevice(m->device));
     hipStream_t s = stream ? static_cast<hipStream_t>(stream) : m->stream;
     if ((rc = ensure_workspace(m, B, S))) return rc;
-    return run_forward(m, ids, mask, B, S, 0, m->ws.out, s, scores, false);
+    return run_forward(m, ids, mask, B, S, 0, m->ws.out, s, scores, nullptr);
 }
 
 int ebh_synchronize(ebh_model* m) {
