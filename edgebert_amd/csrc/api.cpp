@@ -342,7 +342,8 @@ int enqueue_kernels(ebh_model* m, const int* d_ids, const int* d_mask, int B, in
                              w.err, s));
     prof_begin(m, EBH_PROF_EMBED, s, pp, on);
     HIP_TRY(ebh::launch_embed_ln(w.tok_id, w.tok_pos, w.ntok, T, m->word, m->pos, m->type0,
-                                 m->emb_g, m->emb_b, c.vocab_size, H, eps, w.X, w.err, w.X16, s));
+                                 m->emb_g, m->emb_b, c.vocab_size, H, eps, bf16 ? nullptr : w.X, w.err,
+                                 w.X16, s));
     prof_end(m, s, pp, on);
 
     // bf16 models keep the residual stream X in fp32 (LayerNorm, softmax and
@@ -387,7 +388,7 @@ int enqueue_kernels(ebh_model* m, const int* d_ids, const int* d_mask, int B, in
     // outputs that the LayerNorm sums in a fixed order, so the result does not
     // depend on timing.
     auto add_ln = [&](const float* bias, const float* g, const float* b, int parts) -> hipError_t {
-        return bf16 ? ebh::launch_add_layernorm_y16(reinterpret_cast<const uint16_t*>(w.Y), bias, w.X, g, b, T,
+        return bf16 ? ebh::launch_add_layernorm_y16(reinterpret_cast<const uint16_t*>(w.Y), bias, nullptr, g, b, T,
                                                     w.ntok, H, eps, w.X16, s)
                     : ebh::launch_add_layernorm(w.Y, bias, w.X, g, b, T, w.ntok, H, eps, w.X16, s, parts,
                                                 (int64_t)T * H);
@@ -468,7 +469,8 @@ int enqueue_kernels(ebh_model* m, const int* d_ids, const int* d_mask, int B, in
         }
     }
     prof_begin(m, EBH_PROF_POOL, s, pp, on);
-    HIP_TRY(ebh::launch_pool(w.X, w.cu, B, H, S, normalize, d_out, s));
+    HIP_TRY(bf16 ? ebh::launch_pool_b16(w.X16, w.cu, B, H, S, normalize, d_out, s)
+                 : ebh::launch_pool(w.X, w.cu, B, H, S, normalize, d_out, s));
     prof_end(m, s, pp, on);
     if (d_scores) HIP_TRY(ebh::launch_cls_head(d_out, m->cls_w, m->cls_b, B, H, d_scores, s));
     return EBH_OK;
@@ -1215,12 +1217,30 @@ int ebh_op_add_layer_norm_y16(const uint16_t* y, const float* bias, float* x, co
     return EBH_OK;
 }
 
+int ebh_op_add_layer_norm_b16(const uint16_t* y, const float* bias, uint16_t* x16, const float* gamma,
+                              const float* beta, int32_t rows, int32_t H, float eps, void* stream) {
+    if (!y || !bias || !x16 || !gamma || !beta) return fail(EBH_ERR_INVALID_ARG, "null buffer");
+    if (rows < 0 || H <= 0 || !ebh::row4_shape_ok(H)) return fail(EBH_ERR_INVALID_ARG, "bad LayerNorm shape");
+    HIP_TRY(ebh::launch_add_layernorm_y16(y, bias, nullptr, gamma, beta, rows, nullptr, H, eps, x16,
+                                          static_cast<hipStream_t>(stream)));
+    return EBH_OK;
+}
+
 int ebh_op_pool(const float* x, const int32_t* cu_seqlens, int32_t B, int32_t H, int32_t S,
                 int32_t normalize, float* out, void* stream) {
     if (!x || !cu_seqlens || !out) return fail(EBH_ERR_INVALID_ARG, "null buffer");
     if (B < 0 || H <= 0 || H > 2048 || S < 0) return fail(EBH_ERR_INVALID_ARG, "bad pool shape");
     HIP_TRY(ebh::launch_pool(x, cu_seqlens, B, H, S, normalize ? 1 : 0, out,
                              static_cast<hipStream_t>(stream)));
+    return EBH_OK;
+}
+
+int ebh_op_pool_b16(const uint16_t* x16, const int32_t* cu_seqlens, int32_t B, int32_t H, int32_t S,
+                    int32_t normalize, float* out, void* stream) {
+    if (!x16 || !cu_seqlens || !out) return fail(EBH_ERR_INVALID_ARG, "null buffer");
+    if (B < 0 || H <= 0 || H > 2048 || S < 0) return fail(EBH_ERR_INVALID_ARG, "bad pool shape");
+    HIP_TRY(ebh::launch_pool_b16(x16, cu_seqlens, B, H, S, normalize ? 1 : 0, out,
+                                 static_cast<hipStream_t>(stream)));
     return EBH_OK;
 }
 

@@ -84,8 +84,10 @@ hipError_t launch_add_layernorm(const float* y, const float* bias, float* x, con
                                 const float* b, int rows_max, const int* rows_dev, int H, float eps,
                                 uint16_t* x16, hipStream_t s, int nparts = 1,
                                 int64_t part_stride = 0);
-// The same with y stored as bf16 (bf16 models).  Needs 8-byte aligned bf16
-// rows, 16-byte aligned fp32 operands and row4_shape_ok(H).
+// The same with y stored as bf16 (bf16 models).  x == nullptr: the residual
+// stream is bf16 instead, x16 = bf16(LayerNorm((y + bias) + x16)) in place
+// (sums and statistics fp32).  Needs 8-byte aligned bf16 rows, 16-byte aligned
+// fp32 operands and row4_shape_ok(H).
 // H = 4 * L * n with L lanes per row in {64, 32, 16} and n float4 per lane in
 // {1, 2, 3, 4, 6, 8}: the shapes the float4 row kernels take.
 bool row4_shape_ok(int H);
@@ -97,7 +99,8 @@ hipError_t launch_add_layernorm_y16(const uint16_t* y, const float* bias, float*
 hipError_t launch_pack(const int* ids, const int* mask, int B, int S, int* counts, int* cu,
                        int* n_tokens, int* tok_id, int* tok_pos, int* err, hipStream_t s);
 
-// Embedding gather + position + token type 0 + LayerNorm over packed tokens.
+// Embedding gather + position + token type 0 + LayerNorm over packed tokens,
+// into x (fp32) and / or x16 (bf16; either may be nullptr, not both).
 hipError_t launch_embed_ln(const int* tok_id, const int* tok_pos, const int* n_tokens,
                            int T_max, const float* word, const float* pos, const float* type0,
                            const float* g, const float* b, int V, int H, float eps, float* x,
@@ -106,6 +109,9 @@ hipError_t launch_embed_ln(const int* tok_id, const int* tok_pos, const int* n_t
 // Masked mean over each packed sequence, optional L2 normalisation; out [B, H].
 hipError_t launch_pool(const float* x, const int* cu_seqlens, int B, int H, int S,
                        int normalize, float* out, hipStream_t s);
+// The same over a bf16 residual stream x16 (sums in fp32).
+hipError_t launch_pool_b16(const uint16_t* x16, const int* cu_seqlens, int B, int H, int S,
+                           int normalize, float* out, hipStream_t s);
 
 // Cross-encoder head: out[b] = pooled[b] . w + bias[0] (pooled [B, H], w [H]).
 hipError_t launch_cls_head(const float* pooled, const float* w, const float* bias, int B, int H,

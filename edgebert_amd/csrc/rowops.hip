@@ -130,7 +130,7 @@ __device__ __forceinline__ void ln_row(float (&v)[NC], int lane, int H, const fl
         const int i = c * 64 + lane;
         if (i < H) {
             const float o = (v[c] - mean) * inv_std * g[i] + b[i];
-            y[i] = o;
+            if (y) y[i] = o;
             if (y16) y16[i] = f32_to_bf16_rne(o);  // bf16 copy for bf16 GEMM inputs
         }
     }
@@ -211,7 +211,7 @@ __global__ __launch_bounds__(256) void embed_ln_kernel(
         const int i = c * 64 + lane;
         v[c] = i < H ? (wr[i] + pr[i]) + type0[i] : 0.0f;
     }
-    ln_row<NC>(v, lane, H, g, bta, eps, x + (int64_t)t * H, x16 ? x16 + (int64_t)t * H : nullptr);
+    ln_row<NC>(v, lane, H, g, bta, eps, x ? x + (int64_t)t * H : nullptr, x16 ? x16 + (int64_t)t * H : nullptr);
 }
 
 // ---------------------------------------------------------------------------
@@ -259,7 +259,7 @@ __device__ __forceinline__ void ln_row4(float4 (&v)[NV], int sub, int H, const f
         o.y = (v[c].y - mean) * inv_std * g4[c].y + b4[c].y;
         o.z = (v[c].z - mean) * inv_std * g4[c].z + b4[c].z;
         o.w = (v[c].w - mean) * inv_std * g4[c].w + b4[c].w;
-        *reinterpret_cast<float4*>(y + i) = o;
+        if (y) *reinterpret_cast<float4*>(y + i) = o;
         if (y16) {
             uint2 h;
             h.x = (uint32_t)f32_to_bf16_rne(o.x) | ((uint32_t)f32_to_bf16_rne(o.y) << 16);
@@ -338,32 +338,54 @@ EBH_ADD_LN4_KERNEL(add_layernorm4_p4_kernel, 4)    // split-K partials
 // The same with the projection y stored as bf16 (bf16 models write the
 // attention-output and FFN-down products in bf16); the sum, statistics and
 // output stay fp32.
-template <int NV, int LPR>
-__global__ __launch_bounds__(256) void add_layernorm4_y16_kernel(const uint16_t* __restrict__ y,
-                                                                 const float* __restrict__ bias,
-                                                                 float* x, const float* __restrict__ g,
-                                                                 const float* __restrict__ bta,
-                                                                 int rows_max, const int* rows_dev,
-                                                                 int H, float eps, uint16_t* x16) {
+// R16 == false: the residual stream x is fp32 (read, then overwritten with
+// the result, with an optional bf16 copy in x16).  R16: the residual stream is
+// bf16 (bf16 models): x16 is read as the residual and overwritten with the
+// bf16 result; x is not used.  Either way the sums and statistics are fp32.
+template <int NV, int LPR, bool R16>
+__device__ __forceinline__ void add_layernorm4_y16_row(const uint16_t* __restrict__ y, const float* __restrict__ bias,
+                                                       float* x, const float* __restrict__ g,
+                                                       const float* __restrict__ bta, int rows_max,
+                                                       const int* rows_dev, int H, float eps, uint16_t* x16) {
     constexpr int RPB = 256 / LPR;
     const int row = blockIdx.x * RPB + threadIdx.x / LPR, sub = threadIdx.x % LPR;
     const int rows = rows_dev ? *rows_dev : rows_max;
     if (row >= rows) return;
     const uint16_t* yr = y + (int64_t)row * H;
-    float* xr = x + (int64_t)row * H;
+    float* xr = R16 ? nullptr : x + (int64_t)row * H;
+    uint16_t* x16r = x16 ? x16 + (int64_t)row * H : nullptr;
     float4 v[NV];
 #pragma unroll
     for (int c = 0; c < NV; ++c) {
         const int i = 4 * (c * LPR + sub);
         const uint2 a = *reinterpret_cast<const uint2*>(yr + i);
         const float4 bb = *reinterpret_cast<const float4*>(bias + i);
-        const float4 r = *reinterpret_cast<const float4*>(xr + i);
+        float4 r;
+        if constexpr (R16) {
+            const uint2 h = *reinterpret_cast<const uint2*>(x16r + i);
+            r = make_float4(__uint_as_float(h.x << 16), __uint_as_float(h.x & 0xFFFF0000u),
+                            __uint_as_float(h.y << 16), __uint_as_float(h.y & 0xFFFF0000u));
+        } else {
+            r = *reinterpret_cast<const float4*>(xr + i);
+        }
         const float a0 = __uint_as_float(a.x << 16), a1 = __uint_as_float(a.x & 0xFFFF0000u);
         const float a2 = __uint_as_float(a.y << 16), a3 = __uint_as_float(a.y & 0xFFFF0000u);
         v[c] = make_float4((a0 + bb.x) + r.x, (a1 + bb.y) + r.y, (a2 + bb.z) + r.z, (a3 + bb.w) + r.w);
     }
-    ln_row4<NV, LPR>(v, sub, H, g, bta, eps, xr, x16 ? x16 + (int64_t)row * H : nullptr);
+    ln_row4<NV, LPR>(v, sub, H, g, bta, eps, xr, x16r);
 }
+
+#define EBH_ADD_LN4_Y16_KERNEL(NAME, R16)                                                                \
+    template <int NV, int LPR>                                                                           \
+    __global__ __launch_bounds__(256) void NAME(const uint16_t* __restrict__ y, const float* __restrict__ bias, \
+                                                float* x, const float* __restrict__ g,                   \
+                                                const float* __restrict__ bta, int rows_max,             \
+                                                const int* rows_dev, int H, float eps, uint16_t* x16) {  \
+        add_layernorm4_y16_row<NV, LPR, R16>(y, bias, x, g, bta, rows_max, rows_dev, H, eps, x16);      \
+    }
+EBH_ADD_LN4_Y16_KERNEL(add_layernorm4_y16_kernel, false)   // fp32 residual stream
+EBH_ADD_LN4_Y16_KERNEL(add_layernorm4_b16_kernel, true)    // bf16 residual stream
+#undef EBH_ADD_LN4_Y16_KERNEL
 
 template <int NV, int LPR>
 __global__ __launch_bounds__(256) void embed_ln4_kernel(
@@ -391,7 +413,8 @@ __global__ __launch_bounds__(256) void embed_ln4_kernel(
         const float4 ty = *reinterpret_cast<const float4*>(type0 + i);
         v[c] = make_float4((a.x + p4.x) + ty.x, (a.y + p4.y) + ty.y, (a.z + p4.z) + ty.z, (a.w + p4.w) + ty.w);
     }
-    ln_row4<NV, LPR>(v, sub, H, g, bta, eps, x + (int64_t)t * H, x16 ? x16 + (int64_t)t * H : nullptr);
+    ln_row4<NV, LPR>(v, sub, H, g, bta, eps, x ? x + (int64_t)t * H : nullptr,
+                     x16 ? x16 + (int64_t)t * H : nullptr);
 }
 
 // (LPR, NV) for a row of H floats, or LPR = 0 when the float4 kernels do not apply.
@@ -485,11 +508,15 @@ hipError_t launch_add_layernorm_y16(const uint16_t* y, const float* bias, float*
     if (rows_max <= 0) return hipSuccess;
     int lpr, nv;
     row4_shape(H, lpr, nv);
-    if (!lpr || ((uintptr_t)y & 7) || !al16(bias) || !al16(x) || !al16(g) || !al16(b) ||
-        (x16 && ((uintptr_t)x16 & 7)))
+    if (!lpr || ((uintptr_t)y & 7) || !al16(bias) || (x && !al16(x)) || !al16(g) || !al16(b) ||
+        (x16 && ((uintptr_t)x16 & 7)) || (!x && !x16))
         return hipErrorInvalidValue;
-    EBH_ROW4_DISPATCH(add_layernorm4_y16_kernel, lpr, nv, rows_max, s, y, bias, x, g, b, rows_max,
-                      rows_dev, H, eps, x16);
+    if (x)
+        EBH_ROW4_DISPATCH(add_layernorm4_y16_kernel, lpr, nv, rows_max, s, y, bias, x, g, b, rows_max,
+                          rows_dev, H, eps, x16);
+    else
+        EBH_ROW4_DISPATCH(add_layernorm4_b16_kernel, lpr, nv, rows_max, s, y, bias, x, g, b, rows_max,
+                          rows_dev, H, eps, x16);
     return hipGetLastError();
 }
 
@@ -500,7 +527,8 @@ hipError_t launch_embed_ln(const int* tok_id, const int* tok_pos, const int* n_t
     if (T_max <= 0) return hipSuccess;
     int lpr, nv;
     row4_shape(H, lpr, nv);
-    if (lpr && al16(word) && al16(pos) && al16(type0) && al16(g) && al16(b) && al16(x) &&
+    if (!x && !x16) return hipErrorInvalidValue;
+    if (lpr && al16(word) && al16(pos) && al16(type0) && al16(g) && al16(b) && (!x || al16(x)) &&
         (!x16 || ((uintptr_t)x16 & 7) == 0)) {
         EBH_ROW4_DISPATCH(embed_ln4_kernel, lpr, nv, T_max, s, tok_id, tok_pos, n_tokens, word, pos,
                           type0, g, b, V, H, eps, x, err, x16);
@@ -601,6 +629,106 @@ hipError_t launch_pool(const float* x, const int* cu_seqlens, int B, int H, int 
     else if (nc <= 12) hipLaunchKernelGGL(pool_kernel<12>, grid, block, 0, s, x, cu_seqlens, H, S, normalize, out);
     else if (nc <= 16) hipLaunchKernelGGL(pool_kernel<16>, grid, block, 0, s, x, cu_seqlens, H, S, normalize, out);
     else if (nc <= 32) hipLaunchKernelGGL(pool_kernel<32>, grid, block, 0, s, x, cu_seqlens, H, S, normalize, out);
+    else return hipErrorInvalidValue;
+    return hipGetLastError();
+}
+
+// The same over the bf16 residual stream of bf16 models, with the schedule
+// and summation order of pool_kernel, but each lane loads four consecutive
+// bf16 values (8 bytes: elements 4 (c * 64 + lane) .. +3) so that a wave
+// instruction moves 512 bytes; sums in fp32.
+template <int NC4>
+__global__ __launch_bounds__(64 * POOL_WAVES) void pool_b16_kernel(const uint16_t* __restrict__ x,
+                                                                   const int* __restrict__ cu, int H,
+                                                                   int S, int normalize,
+                                                                   float* __restrict__ out) {
+    __shared__ float4 red[POOL_WAVES - 1][NC4 * 64];
+    const int b = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int start = cu[b], len = cu[b + 1] - start;
+    float4 acc[NC4];
+#pragma unroll
+    for (int c = 0; c < NC4; ++c) acc[c] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    auto add_row = [&](float4 (&a)[NC4], const uint2 (&h)[NC4]) __attribute__((always_inline)) {
+#pragma unroll
+        for (int c = 0; c < NC4; ++c) {
+            a[c].x += __uint_as_float(h[c].x << 16);
+            a[c].y += __uint_as_float(h[c].x & 0xFFFF0000u);
+            a[c].z += __uint_as_float(h[c].y << 16);
+            a[c].w += __uint_as_float(h[c].y & 0xFFFF0000u);
+        }
+    };
+    constexpr int U = 4;  // rows in flight per wave
+    int t = wave;
+    for (; t + (U - 1) * POOL_WAVES < len; t += U * POOL_WAVES) {
+        uint2 v[U][NC4];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const uint16_t* xr = x + (int64_t)(start + t + u * POOL_WAVES) * H;
+#pragma unroll
+            for (int c = 0; c < NC4; ++c) {
+                const int i = 4 * (c * 64 + lane);
+                v[u][c] = i < H ? *reinterpret_cast<const uint2*>(xr + i) : make_uint2(0u, 0u);
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u) add_row(acc, v[u]);
+    }
+    for (; t < len; t += POOL_WAVES) {
+        const uint16_t* xr = x + (int64_t)(start + t) * H;
+        uint2 v[NC4];
+#pragma unroll
+        for (int c = 0; c < NC4; ++c) {
+            const int i = 4 * (c * 64 + lane);
+            v[c] = i < H ? *reinterpret_cast<const uint2*>(xr + i) : make_uint2(0u, 0u);
+        }
+        add_row(acc, v);
+    }
+    if (wave > 0) {
+#pragma unroll
+        for (int c = 0; c < NC4; ++c) red[wave - 1][c * 64 + lane] = acc[c];
+    }
+    __syncthreads();
+    if (wave != 0) return;
+    const float count = fmaxf((float)len, 1.0f);
+    const bool all_masked = (len == 0 && S > 0);
+    float ss = 0.0f;
+#pragma unroll
+    for (int c = 0; c < NC4; ++c) {
+        const int i = 4 * (c * 64 + lane);
+        float4 v = acc[c];
+#pragma unroll
+        for (int w = 0; w < POOL_WAVES - 1; ++w) {
+            const float4 r = red[w][c * 64 + lane];
+            v.x += r.x; v.y += r.y; v.z += r.z; v.w += r.w;
+        }
+        v.x /= count; v.y /= count; v.z /= count; v.w /= count;
+        if (all_masked) v = make_float4(__builtin_nanf(""), __builtin_nanf(""), __builtin_nanf(""), __builtin_nanf(""));
+        acc[c] = v;
+        if (i < H) ss += (v.x * v.x + v.y * v.y) + (v.z * v.z + v.w * v.w);
+    }
+    const float norm = normalize ? fmaxf(sqrtf(wave_sum(ss)), 1e-12f) : 1.0f;
+#pragma unroll
+    for (int c = 0; c < NC4; ++c) {
+        const int i = 4 * (c * 64 + lane);
+        if (i < H) {
+            float4 v = acc[c];
+            if (normalize) { v.x /= norm; v.y /= norm; v.z /= norm; v.w /= norm; }
+            float* o = out + (int64_t)b * H + i;   // the caller's [B, H] buffer: 4-byte stores
+            o[0] = v.x; o[1] = v.y; o[2] = v.z; o[3] = v.w;
+        }
+    }
+}
+
+hipError_t launch_pool_b16(const uint16_t* x16, const int* cu_seqlens, int B, int H, int S, int normalize,
+                           float* out, hipStream_t s) {
+    if (B <= 0) return hipSuccess;
+    if (H % 4 || ((uintptr_t)x16 & 7)) return hipErrorInvalidValue;
+    const int nc4 = (H + 255) / 256;
+    const dim3 grid(B), block(64 * POOL_WAVES);
+    if (nc4 <= 2) hipLaunchKernelGGL(pool_b16_kernel<2>, grid, block, 0, s, x16, cu_seqlens, H, S, normalize, out);
+    else if (nc4 <= 3) hipLaunchKernelGGL(pool_b16_kernel<3>, grid, block, 0, s, x16, cu_seqlens, H, S, normalize, out);
+    else if (nc4 <= 4) hipLaunchKernelGGL(pool_b16_kernel<4>, grid, block, 0, s, x16, cu_seqlens, H, S, normalize, out);
+    else if (nc4 <= 8) hipLaunchKernelGGL(pool_b16_kernel<8>, grid, block, 0, s, x16, cu_seqlens, H, S, normalize, out);
     else return hipErrorInvalidValue;
     return hipGetLastError();
 }

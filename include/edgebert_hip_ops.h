@@ -92,11 +92,22 @@ EBH_API int ebh_op_gemm_add_layer_norm(const float* A, int64_t lda, const float*
 EBH_API int ebh_op_add_layer_norm_y16(const uint16_t* y, const float* bias, float* x, const float* gamma,
                               const float* beta, int32_t rows, int32_t H, float eps, void* stream);
 
+/* The same block end over a bf16 residual stream (bf16 models): x16 =
+ * bf16(LayerNorm((y + bias) + x16)), in place on x16 [rows, H] (bf16 bits);
+ * the sums and statistics are fp32 (src/lib.rs:672-674, 677-679, 980-991).
+ * x16 and y rows 8-byte aligned; H as for ebh_op_add_layer_norm_y16. */
+EBH_API int ebh_op_add_layer_norm_b16(const uint16_t* y, const float* bias, uint16_t* x16, const float* gamma,
+                              const float* beta, int32_t rows, int32_t H, float eps, void* stream);
+
 /* mean_pool (src/lib.rs:993-1010) over packed sequences (+ the normalise tail,
  * src/lib.rs:605-612, when normalize != 0); S is the padded length the caller
  * had (S > 0 and an empty sequence gives NaN, as in the reference). */
 EBH_API int ebh_op_pool(const float* x, const int32_t* cu_seqlens, int32_t B, int32_t H, int32_t S,
                 int32_t normalize, float* out, void* stream);
+/* The same over a bf16 residual stream x16 [T, H] (bf16 bits, 8-byte aligned,
+ * H % 4 == 0); sums in fp32. */
+EBH_API int ebh_op_pool_b16(const uint16_t* x16, const int32_t* cu_seqlens, int32_t B, int32_t H, int32_t S,
+                    int32_t normalize, float* out, void* stream);
 
 /* Token packing: ids / mask [B, S] -> cu_seqlens [B+1], n_tokens [1],
  * tok_id / tok_pos [B*S]; counts [B] is scratch; err [1] is cleared. */

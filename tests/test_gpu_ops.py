@@ -405,6 +405,56 @@ def test_add_layer_norm_bf16_projection(env, H):
                                        ctypes.c_float(1e-12), stream(torch)) == Nn.EBH_ERR_INVALID_ARG
 
 
+@pytest.mark.parametrize("H", [384, 768])
+def test_add_layer_norm_bf16_residual(env, H):
+    """The block end of bf16 models, whose residual stream is bf16: x16 =
+    bf16(LayerNorm((y + b) + x16)) in place, the sums and statistics in fp32.
+    Against the oracle's LayerNorm of the same bf16 values, to bf16 rounding."""
+    torch, eb, Nn, L = env
+    import oracle
+    rng = np.random.default_rng(H + 7)
+    rows = 333
+    y16 = torch.from_numpy(rng.standard_normal((rows, H)).astype(np.float32)).to(torch.bfloat16)
+    x16 = torch.from_numpy(rng.standard_normal((rows, H)).astype(np.float32)).to(torch.bfloat16)
+    b = rng.standard_normal(H).astype(np.float32)
+    g = rng.standard_normal(H).astype(np.float32)
+    beta = rng.standard_normal(H).astype(np.float32)
+    dy, dx16, db, dg, dbeta = y16.cuda(), x16.cuda(), dev(torch, b), dev(torch, g), dev(torch, beta)
+    Nn.check(L.ebh_op_add_layer_norm_b16(vp(dy), vp(db), vp(dx16), vp(dg), vp(dbeta), rows, H,
+                                         ctypes.c_float(1e-12), stream(torch)))
+    torch.cuda.synchronize()
+    want = oracle.layer_norm(((y16.float().numpy() + b) + x16.float().numpy()).astype(np.float32), g, beta, 1e-12)
+    got = dx16.cpu().float().numpy()
+    np.testing.assert_allclose(got, want, rtol=2.0 ** -8, atol=1e-6)   # bf16: 8 significant bits
+    assert L.ebh_op_add_layer_norm_b16(vp(dy), vp(db), vp(dx16), vp(dg), vp(dbeta), rows, 100,
+                                       ctypes.c_float(1e-12), stream(torch)) == Nn.EBH_ERR_INVALID_ARG
+
+
+@pytest.mark.parametrize("normalize", [0, 1])
+def test_pool_bf16(env, normalize):
+    """mean_pool + normalise over a bf16 residual stream: fp32 sums of the bf16
+    values, against float64 on the same values."""
+    torch, eb, Nn, L = env
+    H, S = 768, 64
+    lengths = [1, 5, 64, 0, 33]
+    cu = np.concatenate([[0], np.cumsum(lengths)]).astype(np.int32)
+    x16 = torch.from_numpy(np.random.default_rng(2).standard_normal((cu[-1], H)).astype(np.float32)).to(torch.bfloat16)
+    x = x16.float().numpy()
+    dout = torch.empty((len(lengths), H), device="cuda")
+    dx16, dcu = x16.cuda(), dev(torch, cu)
+    Nn.check(L.ebh_op_pool_b16(vp(dx16), vp(dcu), len(lengths), H, S, normalize, vp(dout), stream(torch)))
+    torch.cuda.synchronize()
+    got = dout.cpu().numpy()
+    for bi, n in enumerate(lengths):
+        if n == 0:
+            assert np.isnan(got[bi]).all()
+            continue
+        want = x[cu[bi]:cu[bi + 1]].astype(np.float64).mean(0)
+        if normalize:
+            want = want / max(np.linalg.norm(want), 1e-12)
+        np.testing.assert_allclose(got[bi], want, rtol=0, atol=2e-6)
+
+
 @pytest.mark.parametrize("normalize", [0, 1])
 def test_pool(env, normalize):
     torch, eb, Nn, L = env

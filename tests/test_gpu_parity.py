@@ -173,3 +173,15 @@ def test_few_token_forwards(eb, oracle_mod, weights_for, model_name, B, S, lo, h
     want = oracle_mod.OracleModel(cfg, w).encode_unpadded(ids, mask, normalize=True)
     err, cos = _report(f"few tokens {model_name} {B}x{S}", got, want)
     assert err <= FP32_MAX_ABS and cos >= FP32_MIN_COS
+
+
+def test_bf16_minilm_padded(eb, oracle_mod, weights_for):
+    """MiniLM shape (head_dim 32) with bf16 GEMMs and a bf16 residual stream, on
+    the padded c2 batch: each sequence against the fp32 oracle's unpadded run."""
+    spec = eb.CONFIGS["c2"]
+    w = weights_for(spec.model)
+    ids, mask, _ = eb.make_inputs(spec)
+    got = gpu_model(eb, spec.model, w, "bf16").encode_ids(ids, mask, normalize=True)
+    want = oracle_mod.OracleModel(spec.model, w).encode_unpadded(ids, mask, normalize=True)
+    _, cos = _report("c2 MiniLM bf16 vs fp32 oracle", got, want)
+    assert cos >= BF16_MIN_COS
