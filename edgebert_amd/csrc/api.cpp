@@ -290,6 +290,9 @@ int ensure_workspace(ebh_model* m, int B, int S) {
     w.out = (float*)(b + oOut);
     w.scores = (float*)(b + oScores);
     HIP_TRY(hipMemset(w.err, 0, 4));
+    // The model's stream does not wait for the null stream: the flag must be
+    // clear before the first forward on this workspace can set it.
+    HIP_TRY(hipStreamSynchronize(nullptr));
     return EBH_OK;
 }
 
@@ -999,6 +1002,7 @@ int ebh_synchronize(ebh_model* m) {
     HIP_TRY(hipMemcpy(&err, m->ws.err, 4, hipMemcpyDeviceToHost));
     if (err) {
         HIP_TRY(hipMemset(m->ws.err, 0, 4));
+        HIP_TRY(hipStreamSynchronize(nullptr));  // cleared before the next forward can set it
         return fail(EBH_ERR_RANGE, "token id out of range for vocab %d", m->cfg.vocab_size);
     }
     return EBH_OK;
