@@ -417,6 +417,89 @@ __global__ __launch_bounds__(256) void embed_ln4_kernel(
                      x16 ? x16 + (int64_t)t * H : nullptr);
 }
 
+// The bf16-residual block end of bf16 models with 16-byte lane accesses:
+// LPR lanes per row, each lane NV8 chunks of 8 consecutive elements at
+// 8 * (c * LPR + sub) .. +7 (H == 8 * NV8 * LPR), so the bf16 product, the
+// bf16 residual and the bf16 result move as uint4 (a wave instruction moves
+// 1 KB).  x16 = bf16(LayerNorm((y + bias) + x16)), sums and statistics fp32.
+template <int NV8, int LPR>
+__global__ __launch_bounds__(256) void add_layernorm8_b16_kernel(const uint16_t* __restrict__ y,
+                                                                 const float* __restrict__ bias,
+                                                                 uint16_t* x16, const float* __restrict__ g,
+                                                                 const float* __restrict__ bta, int rows_max,
+                                                                 const int* rows_dev, int H, float eps) {
+    constexpr int RPB = 256 / LPR;
+    const int row = blockIdx.x * RPB + threadIdx.x / LPR, sub = threadIdx.x % LPR;
+    const int rows = rows_dev ? *rows_dev : rows_max;
+    if (row >= rows) return;
+    const uint16_t* yr = y + (int64_t)row * H;
+    uint16_t* xr = x16 + (int64_t)row * H;
+    uint4 ya[NV8], xa[NV8];
+    float4 bb[NV8][2], g4[NV8][2], b4[NV8][2];
+#pragma unroll
+    for (int c = 0; c < NV8; ++c) {
+        const int i = 8 * (c * LPR + sub);
+        ya[c] = *reinterpret_cast<const uint4*>(yr + i);
+        xa[c] = *reinterpret_cast<const uint4*>(xr + i);
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            bb[c][h] = *reinterpret_cast<const float4*>(bias + i + 4 * h);
+            g4[c][h] = *reinterpret_cast<const float4*>(g + i + 4 * h);
+            b4[c][h] = *reinterpret_cast<const float4*>(bta + i + 4 * h);
+        }
+    }
+    auto lo = [](uint32_t w) { return __uint_as_float(w << 16); };
+    auto hi = [](uint32_t w) { return __uint_as_float(w & 0xFFFF0000u); };
+    float v[NV8][8];
+    float s = 0.0f;
+#pragma unroll
+    for (int c = 0; c < NV8; ++c) {
+        const uint32_t yw[4] = {ya[c].x, ya[c].y, ya[c].z, ya[c].w};
+        const uint32_t xw[4] = {xa[c].x, xa[c].y, xa[c].z, xa[c].w};
+        const float bv[8] = {bb[c][0].x, bb[c][0].y, bb[c][0].z, bb[c][0].w,
+                             bb[c][1].x, bb[c][1].y, bb[c][1].z, bb[c][1].w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            v[c][2 * e] = (lo(yw[e]) + bv[2 * e]) + lo(xw[e]);
+            v[c][2 * e + 1] = (hi(yw[e]) + bv[2 * e + 1]) + hi(xw[e]);
+        }
+#pragma unroll
+        for (int e = 0; e < 8; e += 2) s += v[c][e] + v[c][e + 1];
+    }
+    const float mean = group_sum<LPR>(s) / (float)H;
+    float ss = 0.0f;
+#pragma unroll
+    for (int c = 0; c < NV8; ++c)
+#pragma unroll
+        for (int e = 0; e < 8; e += 2) {
+            const float d0 = v[c][e] - mean, d1 = v[c][e + 1] - mean;
+            ss += d0 * d0 + d1 * d1;
+        }
+    const float inv_std = 1.0f / sqrtf(group_sum<LPR>(ss) / (float)H + eps);
+#pragma unroll
+    for (int c = 0; c < NV8; ++c) {
+        const float gv[8] = {g4[c][0].x, g4[c][0].y, g4[c][0].z, g4[c][0].w,
+                             g4[c][1].x, g4[c][1].y, g4[c][1].z, g4[c][1].w};
+        const float tv[8] = {b4[c][0].x, b4[c][0].y, b4[c][0].z, b4[c][0].w,
+                             b4[c][1].x, b4[c][1].y, b4[c][1].z, b4[c][1].w};
+        uint32_t o[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+            o[e] = pack_bf16x2((v[c][2 * e] - mean) * inv_std * gv[2 * e] + tv[2 * e],
+                               (v[c][2 * e + 1] - mean) * inv_std * gv[2 * e + 1] + tv[2 * e + 1]);
+        *reinterpret_cast<uint4*>(xr + 8 * (c * LPR + sub)) = make_uint4(o[0], o[1], o[2], o[3]);
+    }
+}
+
+// (LPR, NV8) for add_layernorm8_b16_kernel, or LPR = 0.
+static void row8_shape(int H, int& lpr, int& nv8) {
+    lpr = 0;
+    nv8 = 0;
+    const int cands[3] = {64, 32, 16};
+    for (int c : cands)
+        if (H % (8 * c) == 0 && H / (8 * c) >= 1 && H / (8 * c) <= 4) { lpr = c; nv8 = H / (8 * c); return; }
+}
+
 // (LPR, NV) for a row of H floats, or LPR = 0 when the float4 kernels do not apply.
 static void row4_shape(int H, int& lpr, int& nv) {
     lpr = 0;
@@ -511,6 +594,22 @@ hipError_t launch_add_layernorm_y16(const uint16_t* y, const float* bias, float*
     if (!lpr || ((uintptr_t)y & 7) || !al16(bias) || (x && !al16(x)) || !al16(g) || !al16(b) ||
         (x16 && ((uintptr_t)x16 & 7)) || (!x && !x16))
         return hipErrorInvalidValue;
+    int lpr8, nv8;
+    row8_shape(H, lpr8, nv8);
+    if (!x && lpr8 && ((uintptr_t)y & 15) == 0 && ((uintptr_t)x16 & 15) == 0 && ((uintptr_t)g & 15) == 0 &&
+        ((uintptr_t)b & 15) == 0 && ((uintptr_t)bias & 15) == 0) {
+        const dim3 grid8((rows_max + 256 / lpr8 - 1) / (256 / lpr8));
+#define EBH_LN8(L, N)                                                                                  \
+        if (lpr8 == L && nv8 == N) {                                                                    \
+            hipLaunchKernelGGL((add_layernorm8_b16_kernel<N, L>), grid8, dim3(256), 0, s, y, bias, x16, g, b, \
+                               rows_max, rows_dev, H, eps);                                            \
+            return hipGetLastError();                                                                  \
+        }
+        EBH_LN8(64, 1) EBH_LN8(64, 2) EBH_LN8(64, 3) EBH_LN8(64, 4)
+        EBH_LN8(32, 1) EBH_LN8(32, 2) EBH_LN8(32, 3) EBH_LN8(32, 4)
+        EBH_LN8(16, 1) EBH_LN8(16, 2) EBH_LN8(16, 3) EBH_LN8(16, 4)
+#undef EBH_LN8
+    }
     if (x)
         EBH_ROW4_DISPATCH(add_layernorm4_y16_kernel, lpr, nv, rows_max, s, y, bias, x, g, b, rows_max,
                           rows_dev, H, eps, x16);
