@@ -879,8 +879,9 @@ __global__ __launch_bounds__(256) void gemm_bf16_kernel(GemmArgs p) {
 // ---------------------------------------------------------------------------
 // Few-token products (M_max <= 64: a handful of short sentences).  Such a
 // product is a chain of memory round trips rather than MFMA work, so each
-// operand byte is read once and the work is spread over as many workgroups
-// as the shape gives: workgroup (32-column slice, 16-row block, k split s)
+// weight byte is read once per 16-row block (the few activation rows stay in
+// cache) and the work is spread over as many workgroups as the shape gives:
+// workgroup (32-column slice, 16-row block, k split s)
 // runs NW waves, wave w taking k in [s*K/S + w*KW, s*K/S + (w+1)*KW), KW =
 // K / (NW*S), with all of a wave's loads in flight at once when KW <=
 // 16*NSTEP.  v_mfma_f32_16x16x4_f32: lane l gives A row l % 16 and W row
