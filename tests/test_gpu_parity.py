@@ -185,3 +185,22 @@ def test_bf16_minilm_padded(eb, oracle_mod, weights_for):
     want = oracle_mod.OracleModel(spec.model, w).encode_unpadded(ids, mask, normalize=True)
     _, cos = _report("c2 MiniLM bf16 vs fp32 oracle", got, want)
     assert cos >= BF16_MIN_COS
+
+
+@pytest.mark.parametrize("B,S,lo,hi", [(1, 1, 1, 1), (2, 8, 8, 8), (5, 12, 3, 12)])
+def test_bf16_minilm_few_tokens(eb, oracle_mod, weights_for, B, S, lo, hi):
+    """bf16 MiniLM at a handful of tokens: bf16 GEMM tiles far larger than the
+    packed rows, a single ragged row block, and the bf16 pool's half-used
+    second chunk (H = 384).  Each sequence against the fp32 oracle's unpadded
+    run; repeated calls (graph replays) give bit-identical vectors."""
+    from edgebert_amd.synth import InputSpec, MINILM_L6, make_inputs
+    spec = InputSpec(f"few16_{B}x{S}", MINILM_L6, B, S, lo, hi, 40 + B * S)
+    w = weights_for(MINILM_L6)
+    ids, mask, _ = make_inputs(spec)
+    m = gpu_model(eb, MINILM_L6, w, "bf16")
+    got = m.encode_ids(ids, mask, normalize=True)
+    for _ in range(2):
+        assert np.array_equal(m.encode_ids(ids, mask, normalize=True), got)
+    want = oracle_mod.OracleModel(MINILM_L6, w).encode_unpadded(ids, mask, normalize=True)
+    _, cos = _report(f"bf16 MiniLM few tokens {B}x{S}", got, want)
+    assert cos >= BF16_MIN_COS
