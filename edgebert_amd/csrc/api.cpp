@@ -14,6 +14,7 @@
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <mutex>
 #include <string>
@@ -89,6 +90,7 @@ struct GraphEntry {
     int B, S, normalize, host;
     const void *ids, *mask;
     void *out, *scores;
+    int64_t tokens;                   // host calls: the exact token count; else -1
     int seen;                         // calls with this key; -1: recording failed
     hipGraphExec_t exec;              // recorded at the key's second call
     uint64_t used;
@@ -328,15 +330,17 @@ int ensure_host_staging(ebh_model* m, HostSlot& hs, int64_t T, int64_t outn) {
 // The kernels of one forward on stream s (ids/mask already in device memory).
 // d_scores (optional, cross-encoders): score[b] = pooled[b] . w + bias, from
 // the un-normalised pooled rows left in d_out.
+// tokens: the number of mask == 1 tokens when the host knows it (the
+// blocking entry points), else -1.
 int enqueue_kernels(ebh_model* m, const int* d_ids, const int* d_mask, int B, int S,
-                    int normalize, float* d_out, hipStream_t s, float* d_scores) {
+                    int normalize, float* d_out, hipStream_t s, float* d_scores, int64_t tokens) {
     const ebh_config& c = m->cfg;
     const int H = c.hidden_size, I = c.intermediate_size, nh = c.num_attention_heads;
     const int hd = H / nh;
     const float eps = c.layer_norm_eps;
     const float scale = 1.0f / sqrtf((float)hd);  // src/lib.rs:196-197
     Workspace& w = m->ws;
-    const int T = B * S;
+    const int T = B * S;  // rows every kernel is sized for; they read the packed count on the device
 
     ProfPair pp{};
     bool on = false;
@@ -357,10 +361,12 @@ int enqueue_kernels(ebh_model* m, const int* d_ids, const int* d_mask, int B, in
     uint16_t* ctx16 = reinterpret_cast<uint16_t*>(w.CTX);
     uint16_t* f16 = reinterpret_cast<uint16_t*>(w.F);
     auto gemm = [&](int kind, const void* A, int64_t lda, const float* W32, const uint16_t* W16,
-                    const float* bias, void* C, int N, int K, int epi, bool c16, int splits = 1) -> int {
+                    const float* bias, void* C, int N, int K, int epi, bool c16, int splits = 1,
+                    int rows = -1) -> int {
+        if (rows < 0) rows = T;
         ebh::GemmArgs a{};
         a.splits = splits;
-        a.split_stride = (int64_t)T * N;
+        a.split_stride = (int64_t)rows * N;
         a.A = A;
         a.W = bf16 ? (const void*)W16 : (const void*)W32;
         a.bias = bias;
@@ -370,7 +376,7 @@ int enqueue_kernels(ebh_model* m, const int* d_ids, const int* d_mask, int B, in
         a.ldw = K;
         a.ldr = 0;
         a.ldc = N;
-        a.M_max = T;
+        a.M_max = rows;
         a.M_dev = w.ntok;
         a.N = N;
         a.K = K;
@@ -390,25 +396,32 @@ int enqueue_kernels(ebh_model* m, const int* d_ids, const int* d_mask, int B, in
     // With few tokens (fp32) these two products are split over K into partial
     // outputs that the LayerNorm sums in a fixed order, so the result does not
     // depend on timing.
+    // fp32 with at least a 128-row block per CU: the attention-output and
+    // FFN-down products end in their bias + residual + LayerNorm inside the
+    // GEMM (each workgroup holds whole rows), in place on X.  That form runs
+    // one 128-row block per workgroup, so a ragged batch whose packed rows
+    // (known here when the host counted them) fill too few blocks takes the
+    // split path instead, with these two products and their LayerNorms sized
+    // for the packed rows; everything else stays sized for B*S.
+    const int T_real = tokens >= 0 && tokens < T ? (int)tokens : T;
+    const bool flip = !bf16 && ebh::gemm_f32_add_ln_fits(T, H, H) && !ebh::gemm_f32_add_ln_fits(T_real, H, H);
+    const int T_od = flip ? T_real : T;
+    const bool fuse_out = !bf16 && ebh::gemm_f32_add_ln_fits(T_od, H, H);
+    const bool fuse_down = !bf16 && ebh::gemm_f32_add_ln_fits(T_od, H, I);
     auto add_ln = [&](const float* bias, const float* g, const float* b, int parts) -> hipError_t {
-        return bf16 ? ebh::launch_add_layernorm_y16(reinterpret_cast<const uint16_t*>(w.Y), bias, nullptr, g, b, T,
+        return bf16 ? ebh::launch_add_layernorm_y16(reinterpret_cast<const uint16_t*>(w.Y), bias, nullptr, g, b, T_od,
                                                     w.ntok, H, eps, w.X16, s)
-                    : ebh::launch_add_layernorm(w.Y, bias, w.X, g, b, T, w.ntok, H, eps, w.X16, s, parts,
-                                                (int64_t)T * H);
+                    : ebh::launch_add_layernorm(w.Y, bias, w.X, g, b, T_od, w.ntok, H, eps, w.X16, s, parts,
+                                                (int64_t)T_od * H);
     };
-    const int64_t part_cap = (int64_t)w.y_parts * w.tok_cap / std::max<int64_t>(T, 1);
+    const int64_t part_cap = (int64_t)w.y_parts * w.tok_cap / std::max<int64_t>(T_od, 1);
     auto splits_for = [&](int K) {
         if (bf16) return 1;
-        int sp = ebh::gemm_f32_splits(T, H, K);
+        int sp = ebh::gemm_f32_splits(T_od, H, K);
         while (sp > 1 && sp > part_cap) sp /= 2;
         return sp;
     };
     const int sp_out = splits_for(H), sp_down = splits_for(I);
-    // fp32 with at least a 128-row block per CU: the attention-output and
-    // FFN-down products end in their bias + residual + LayerNorm inside the
-    // GEMM (each workgroup holds whole rows), in place on X.
-    const bool fuse_out = !bf16 && ebh::gemm_f32_add_ln_fits(T, H, H);
-    const bool fuse_down = !bf16 && ebh::gemm_f32_add_ln_fits(T, H, I);
     auto gemm_ln = [&](int kind, const float* A, const float* W, const float* bias, const float* g,
                        const float* b, int K) -> int {
         ebh::GemmArgs a{};
@@ -451,7 +464,7 @@ int enqueue_kernels(ebh_model* m, const int* d_ids, const int* d_mask, int B, in
             if ((rc = gemm_ln(EBH_PROF_GEMM_OUT, w.CTX, L.wo, L.bo, L.ln1_g, L.ln1_b, H))) return rc;
         } else {
             if ((rc = gemm(EBH_PROF_GEMM_OUT, bf16 ? (const void*)ctx16 : w.CTX, H, L.wo, L.wo16, nullptr,
-                           w.Y, H, H, ebh::EPI_NONE, bf16, sp_out)))
+                           w.Y, H, H, ebh::EPI_NONE, bf16, sp_out, T_od)))
                 return rc;
             prof_begin(m, EBH_PROF_LAYERNORM, s, pp, on);
             HIP_TRY(add_ln(L.bo, L.ln1_g, L.ln1_b, sp_out));
@@ -464,7 +477,7 @@ int enqueue_kernels(ebh_model* m, const int* d_ids, const int* d_mask, int B, in
             if ((rc = gemm_ln(EBH_PROF_GEMM_FFN_DOWN, w.F, L.w2, L.b2, L.ln2_g, L.ln2_b, I))) return rc;
         } else {
             if ((rc = gemm(EBH_PROF_GEMM_FFN_DOWN, bf16 ? (const void*)f16 : w.F, I, L.w2, L.w216, nullptr,
-                           w.Y, H, I, ebh::EPI_NONE, bf16, sp_down)))
+                           w.Y, H, I, ebh::EPI_NONE, bf16, sp_down, T_od)))
                 return rc;
             prof_begin(m, EBH_PROF_LAYERNORM, s, pp, on);
             HIP_TRY(add_ln(L.b2, L.ln2_g, L.ln2_b, sp_down));
@@ -490,6 +503,7 @@ hipGraphExec_t graph_for(ebh_model* m, const GraphEntry& key, hipStream_t s, Bod
     GraphEntry* e = nullptr;
     for (auto& g : m->graphs)
         if (g.B == key.B && g.S == key.S && g.normalize == key.normalize && g.host == key.host &&
+            g.tokens == key.tokens &&
             g.ids == key.ids && g.mask == key.mask && g.out == key.out && g.scores == key.scores) {
             e = &g;
             break;
@@ -532,7 +546,7 @@ hipGraphExec_t graph_for(ebh_model* m, const GraphEntry& key, hipStream_t s, Bod
 // buffers, and the result (d_scores if given, else d_out) and the id-range
 // flag go back to it.
 int run_forward(ebh_model* m, const int* d_ids, const int* d_mask, int B, int S, int normalize,
-                float* d_out, hipStream_t s, float* d_scores, HostSlot* hs) {
+                float* d_out, hipStream_t s, float* d_scores, HostSlot* hs, int64_t tokens = -1) {
     const bool host = hs != nullptr;
     Workspace& w = m->ws;
     const int64_t T = (int64_t)B * S;
@@ -543,7 +557,7 @@ int run_forward(ebh_model* m, const int* d_ids, const int* d_mask, int B, int S,
             HIP_TRY(hipMemcpyAsync(w.ids, hs->ids, T * 4, hipMemcpyHostToDevice, st));
             HIP_TRY(hipMemcpyAsync(w.mask, hs->mask, T * 4, hipMemcpyHostToDevice, st));
         }
-        int rc = enqueue_kernels(m, d_ids, d_mask, B, S, normalize, d_out, st, d_scores);
+        int rc = enqueue_kernels(m, d_ids, d_mask, B, S, normalize, d_out, st, d_scores, tokens);
         if (rc) return rc;
         if (host) {
             HIP_TRY(hipMemcpyAsync(hs->out, d_scores ? d_scores : d_out, n_out * 4, hipMemcpyDeviceToHost, st));
@@ -555,7 +569,7 @@ int run_forward(ebh_model* m, const int* d_ids, const int* d_mask, int B, int S,
     // has its own.
     const GraphEntry key{B, S, normalize, host ? 1 : 0, host ? (const void*)hs->ids : d_ids,
                          host ? (const void*)hs->mask : d_mask, host ? (void*)hs->out : d_out, d_scores,
-                         0, nullptr, 0};
+                         tokens, 0, nullptr, 0};
     if (hipGraphExec_t exec = graph_for(m, key, s, body)) {
         HIP_TRY(hipGraphLaunch(exec, s));
     } else {
@@ -587,9 +601,11 @@ int host_forward(ebh_model* m, int B, int S, int normalize, float* out, bool sco
         int rc = ensure_host_staging(m, hs, T, (int64_t)B * H);
         if (rc) return rc;
         if ((rc = stage(hs.ids, hs.mask))) return rc;
+        int64_t tokens = 0;
+        for (int64_t i = 0; i < T; ++i) tokens += hs.mask[i] != 0;
         if ((rc = ensure_workspace(m, B, S))) return rc;
         if ((rc = run_forward(m, m->ws.ids, m->ws.mask, B, S, normalize, m->ws.out, m->stream,
-                              score ? m->ws.scores : nullptr, &hs)))
+                              score ? m->ws.scores : nullptr, &hs, tokens)))
             return rc;
     }
     HIP_TRY(hipEventSynchronize(hs.done));

@@ -204,3 +204,22 @@ def test_bf16_minilm_few_tokens(eb, oracle_mod, weights_for, B, S, lo, hi):
     want = oracle_mod.OracleModel(MINILM_L6, w).encode_unpadded(ids, mask, normalize=True)
     _, cos = _report(f"bf16 MiniLM few tokens {B}x{S}", got, want)
     assert cos >= BF16_MIN_COS
+
+
+def test_ragged_large_batch_host_path(eb, oracle_mod, weights_for):
+    """256 sentences of 8..128 tokens padded to 128 through the host-buffer
+    entry point: the host counts the packed rows (about half of B*S), too few
+    128-row blocks for the fused GEMM + LayerNorm, so the attention-output and
+    FFN-down products take the split path sized for the real rows.  16
+    sequences against the oracle's unpadded run; every row unit-norm."""
+    from edgebert_amd.synth import InputSpec, MINILM_L6, make_inputs
+    spec = InputSpec("ragged256", MINILM_L6, 256, 128, 8, 128, 77)
+    w = weights_for(MINILM_L6)
+    ids, mask, _ = make_inputs(spec)
+    assert int(mask.sum()) < 256 * 128 // 2 + 4096
+    got = gpu_model(eb, MINILM_L6, w).encode_ids(ids, mask, normalize=True)
+    np.testing.assert_allclose(np.linalg.norm(got.astype(np.float64), axis=1), 1.0, atol=1e-5)
+    sel = np.arange(0, 256, 16)
+    want = oracle_mod.OracleModel(MINILM_L6, w).encode_unpadded(ids[sel], mask[sel], normalize=True)
+    err, cos = _report("ragged 256 host path", got[sel], want)
+    assert err <= FP32_MAX_ABS and cos >= FP32_MIN_COS
