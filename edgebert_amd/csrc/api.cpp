@@ -345,18 +345,27 @@ int enqueue_kernels(ebh_model* m, const int* d_ids, const int* d_mask, int B, in
     ProfPair pp{};
     bool on = false;
     const bool bf16 = m->dtype == EBH_DTYPE_BF16;
-    HIP_TRY(ebh::launch_pack(d_ids, d_mask, B, S, w.counts, w.cu, w.ntok, w.tok_id, w.tok_pos,
-                             w.err, s));
-    prof_begin(m, EBH_PROF_EMBED, s, pp, on);
-    HIP_TRY(ebh::launch_embed_ln(w.tok_id, w.tok_pos, w.ntok, T, m->word, m->pos, m->type0,
-                                 m->emb_g, m->emb_b, c.vocab_size, H, eps, bf16 ? nullptr : w.X, w.err,
-                                 w.X16, s));
-    prof_end(m, s, pp, on);
+    if (ebh::pack_embed_few_fits(B, S, H)) {   // a few short sentences: one launch
+        prof_begin(m, EBH_PROF_EMBED, s, pp, on);
+        HIP_TRY(ebh::launch_pack_embed_few(d_ids, d_mask, B, S, w.cu, w.ntok, w.tok_id, w.tok_pos, w.err,
+                                           m->word, m->pos, m->type0, m->emb_g, m->emb_b, c.vocab_size, H,
+                                           eps, bf16 ? nullptr : w.X, w.X16, s));
+        prof_end(m, s, pp, on);
+    } else {
+        HIP_TRY(ebh::launch_pack(d_ids, d_mask, B, S, w.counts, w.cu, w.ntok, w.tok_id, w.tok_pos,
+                                 w.err, s));
+        prof_begin(m, EBH_PROF_EMBED, s, pp, on);
+        HIP_TRY(ebh::launch_embed_ln(w.tok_id, w.tok_pos, w.ntok, T, m->word, m->pos, m->type0,
+                                     m->emb_g, m->emb_b, c.vocab_size, H, eps, bf16 ? nullptr : w.X, w.err,
+                                     w.X16, s));
+        prof_end(m, s, pp, on);
+    }
 
-    // bf16 models keep the residual stream X in fp32 (LayerNorm, softmax and
-    // every sum stay fp32) and hand the GEMMs bf16 operands: X16 (written by
-    // each LayerNorm), q / k / v, the attention context and the GELU output,
-    // each stored as bf16 in the first half of its fp32 buffer.
+    // bf16 models keep the residual stream in bf16 (X16, written by each
+    // LayerNorm; every sum and statistic stays fp32) and hand the GEMMs bf16
+    // operands: X16, q / k / v, the attention context and the GELU output,
+    // each of the last three stored as bf16 in the first half of its fp32
+    // buffer.
     uint16_t* qkv16 = reinterpret_cast<uint16_t*>(w.QKV);
     uint16_t* ctx16 = reinterpret_cast<uint16_t*>(w.CTX);
     uint16_t* f16 = reinterpret_cast<uint16_t*>(w.F);

@@ -99,6 +99,14 @@ hipError_t launch_add_layernorm_y16(const uint16_t* y, const float* bias, float*
 hipError_t launch_pack(const int* ids, const int* mask, int B, int S, int* counts, int* cu,
                        int* n_tokens, int* tok_id, int* tok_pos, int* err, hipStream_t s);
 
+// Packing and embeddings in one launch for B*S <= 64 positions (the float4 row
+// shapes): the same outputs as launch_pack followed by launch_embed_ln.
+bool pack_embed_few_fits(int B, int S, int H);
+hipError_t launch_pack_embed_few(const int* ids, const int* mask, int B, int S, int* cu, int* n_tokens,
+                                 int* tok_id, int* tok_pos, int* err, const float* word, const float* pos,
+                                 const float* type0, const float* g, const float* b, int V, int H, float eps,
+                                 float* x, uint16_t* x16, hipStream_t s);
+
 // Embedding gather + position + token type 0 + LayerNorm over packed tokens,
 // into x (fp32) and / or x16 (bf16; either may be nullptr, not both).
 hipError_t launch_embed_ln(const int* tok_id, const int* tok_pos, const int* n_tokens,

@@ -640,6 +640,88 @@ hipError_t launch_embed_ln(const int* tok_id, const int* tok_pos, const int* n_t
 }
 
 // ---------------------------------------------------------------------------
+// Token packing and embeddings in one launch for at most 64 positions (B*S <=
+// 64: a few short sentences, where four separate launches cost more than
+// their work).  A token's packed index is the number of mask == 1 positions
+// before it in row-major order, so one wave ballot over the <= 64 mask values
+// gives every index, cu_seqlens and the count.  Every workgroup takes the
+// ballot itself (the mask is at most 64 ints) and embeds its own rows of the
+// packed order; workgroup 0 also writes cu_seqlens, n_tokens, tok_id /
+// tok_pos and the id-range flag, as a plain store of "some id out of range",
+// so no clear has to be ordered before another workgroup's report.
+// ---------------------------------------------------------------------------
+template <int NV, int LPR>
+__global__ __launch_bounds__(256) void pack_embed_few_kernel(
+    const int* __restrict__ ids, const int* __restrict__ mask, int B, int S, int* __restrict__ cu,
+    int* __restrict__ n_tokens, int* __restrict__ tok_id, int* __restrict__ tok_pos, int* __restrict__ err,
+    const float* __restrict__ word, const float* __restrict__ pos, const float* __restrict__ type0,
+    const float* __restrict__ g, const float* __restrict__ bta, int V, int H, float eps, float* __restrict__ x,
+    uint16_t* __restrict__ x16) {
+    const int T = B * S;                          // <= 64
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const bool in = lane < T;
+    const int id_l = in ? ids[lane] : 0;
+    const bool on = in && mask[lane] != 0;
+    const unsigned long long bal = __ballot(on);
+    const unsigned long long bad = __ballot(on && (id_l < 0 || id_l >= V));
+    const int n = __popcll(bal);
+    if (blockIdx.x == 0 && wave == 0) {
+        const unsigned long long below = lane ? (bal & (~0ull >> (64 - lane))) : 0ull;
+        if (on) {
+            const int k = __popcll(below);
+            tok_id[k] = id_l;
+            tok_pos[k] = lane % S;
+        }
+        if (lane < B) cu[lane] = __popcll(bal & ((1ull << (lane * S)) - 1));  // lane * S <= 63
+        if (lane == 0) {
+            cu[B] = n;
+            *n_tokens = n;
+            *err = bad != 0ull;
+        }
+    }
+    constexpr int RPB = 256 / LPR;
+    const int r = blockIdx.x * RPB + tid / LPR, sub = tid % LPR;
+    if (r >= n) return;
+    unsigned long long rest = bal;                // position of the r-th mask == 1 entry
+    for (int i = 0; i < r; ++i) rest &= rest - 1;
+    const int t = __builtin_ctzll(rest);
+    int id = ids[t];
+    if (id < 0 || id >= V) id = 0;                // reported through err above
+    const float* wr = word + (int64_t)id * H;
+    const float* pr = pos + (int64_t)(t % S) * H;
+    float4 v[NV];
+#pragma unroll
+    for (int c = 0; c < NV; ++c) {
+        const int i = 4 * (c * LPR + sub);
+        const float4 a = *reinterpret_cast<const float4*>(wr + i);
+        const float4 p4 = *reinterpret_cast<const float4*>(pr + i);
+        const float4 ty = *reinterpret_cast<const float4*>(type0 + i);
+        v[c] = make_float4((a.x + p4.x) + ty.x, (a.y + p4.y) + ty.y, (a.z + p4.z) + ty.z, (a.w + p4.w) + ty.w);
+    }
+    ln_row4<NV, LPR>(v, sub, H, g, bta, eps, x ? x + (int64_t)r * H : nullptr, x16 ? x16 + (int64_t)r * H : nullptr);
+}
+
+bool pack_embed_few_fits(int B, int S, int H) {
+    int lpr, nv;
+    row4_shape(H, lpr, nv);
+    return B > 0 && S > 0 && B * S <= 64 && lpr != 0;
+}
+
+hipError_t launch_pack_embed_few(const int* ids, const int* mask, int B, int S, int* cu, int* n_tokens,
+                                 int* tok_id, int* tok_pos, int* err, const float* word, const float* pos,
+                                 const float* type0, const float* g, const float* b, int V, int H, float eps,
+                                 float* x, uint16_t* x16, hipStream_t s) {
+    int lpr, nv;
+    row4_shape(H, lpr, nv);
+    if (!pack_embed_few_fits(B, S, H) || (!x && !x16) || !al16(word) || !al16(pos) || !al16(type0) || !al16(g) ||
+        !al16(b) || (x && !al16(x)) || (x16 && ((uintptr_t)x16 & 7)))
+        return hipErrorInvalidValue;
+    EBH_ROW4_DISPATCH(pack_embed_few_kernel, lpr, nv, B * S, s, ids, mask, B, S, cu, n_tokens, tok_id, tok_pos,
+                      err, word, pos, type0, g, b, V, H, eps, x, x16);
+    return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
 // mean_pool (src/lib.rs:993-1010) + normalise (src/lib.rs:605-612): one
 // 512-thread workgroup per sequence.  Wave w sums tokens w, w+8, w+16, ...
 // with four rows in flight per step (the sum is latency-bound otherwise);
