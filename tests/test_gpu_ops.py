@@ -584,13 +584,16 @@ def test_all_masked_row_is_nan_others_unchanged(env, minilm, orc):
     assert np.abs(got[[0, 2]] - want[[0, 2]]).max() <= 1e-4
 
 
-def test_mask_with_holes_matches_padded_oracle(env, minilm, orc):
-    """Left padding and holes: positions stay absolute, as in the reference."""
-    rng = np.random.default_rng(9)
-    ids = rng.integers(1000, 30522, (6, 40)).astype(np.float32)
-    mask = (rng.random((6, 40)) < 0.7).astype(np.float32)
-    mask[0, :10] = 0          # left padded
-    mask[:, 5] = 1
+@pytest.mark.parametrize("B,S", [(6, 40), (4, 16), (3, 7)])
+def test_mask_with_holes_matches_padded_oracle(env, minilm, orc, B, S):
+    """Left padding and holes: positions stay absolute, as in the reference.
+    At most 64 positions (4 x 16, 3 x 7) the packing runs in the fused
+    packing + embeddings kernel."""
+    rng = np.random.default_rng(9 + B * S)
+    ids = rng.integers(1000, 30522, (B, S)).astype(np.float32)
+    mask = (rng.random((B, S)) < 0.7).astype(np.float32)
+    mask[0, :S // 4] = 0      # left padded
+    mask[:, S // 2] = 1
     got = minilm.forward(ids, mask)
     want = orc.forward(ids, mask)
     assert np.abs(got - want).max() <= 1e-4
