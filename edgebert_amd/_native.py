@@ -88,6 +88,8 @@ _SIGS = {
     "ebh_op_embed_ln": (_i32, [_vp, _vp, _vp, _i32, _vp, _vp, _vp, _vp, _vp, _i32, _i32, _f32,
                                _vp, _vp, _vp]),
     "ebh_op_f32_to_bf16": (_i32, [_vp, _vp, _i64, _vp]),
+    "ebh_op_widen16": (_i32, [_vp, _vp, _i64, _i32, _vp]),
+    "ebh_op_gelu": (_i32, [_vp, _vp, _i64, _vp]),
 }
 
 _LIB = None

@@ -16,6 +16,7 @@
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <memory>
 #include <mutex>
 #include <string>
 #include <unordered_map>
@@ -57,9 +58,21 @@ using ebh::set_error;
 constexpr size_t kAlign = 256;
 size_t align_up(size_t x) { return (x + kAlign - 1) / kAlign * kAlign; }
 
+// A tensor handed over before ebh_finalize, in its checkpoint encoding: a
+// copy of the caller's f32 data (ebh_set_tensor), or a view of F32 / F16 /
+// BF16 elements inside a mapped safetensors file (`keep` holds the mapping).
+// ebh_finalize uploads each one straight into its place in the device block.
 struct HostTensor {
-    std::vector<float> data;
     std::vector<int64_t> shape;
+    int kind = ebh::TENSOR_F32;
+    const void* src = nullptr;
+    std::vector<float> own;
+    std::shared_ptr<const void> keep;
+    int64_t count() const {
+        int64_t n = 1;
+        for (int64_t d : shape) n *= d;
+        return n;
+    }
 };
 
 struct DevLayer {
@@ -105,7 +118,6 @@ struct HostSlot {
     int* ids = nullptr;
     int* mask = nullptr;
     float* out = nullptr;
-    int* err = nullptr;
     int64_t cap = 0, out_cap = 0;
     hipEvent_t done = nullptr;  // completion of this slot's last forward
     std::mutex mu;
@@ -261,9 +273,12 @@ int ensure_workspace(ebh_model* m, int B, int S) {
                  oNtok = take(4), oTid = take(tcap * 4), oTpos = take(tcap * 4), oErr = take(4),
                  oOut = take((size_t)bcap * H * 4), oScores = take((size_t)bcap * 4);
     // Work from the previous call may still use the old block, and recorded
-    // forwards hold its addresses.
+    // forwards hold its addresses.  A raised id-range flag is carried over to
+    // the new block (it stays raised until ebh_synchronize reads it).
     if (m->has_done) HIP_TRY(hipEventSynchronize(m->done));
     drop_graphs(m);
+    int old_err = 0;
+    if (w.base) HIP_TRY(hipMemcpy(&old_err, w.err, 4, hipMemcpyDeviceToHost));
     if (w.base) HIP_TRY(hipFree(w.base));
     w.base = nullptr;
     w.tok_cap = 0;
@@ -291,9 +306,9 @@ int ensure_workspace(ebh_model* m, int B, int S) {
     w.err = (int*)(b + oErr);
     w.out = (float*)(b + oOut);
     w.scores = (float*)(b + oScores);
-    HIP_TRY(hipMemset(w.err, 0, 4));
+    HIP_TRY(hipMemcpy(w.err, &old_err, 4, hipMemcpyHostToDevice));
     // The model's stream does not wait for the null stream: the flag must be
-    // clear before the first forward on this workspace can set it.
+    // written before the first forward on this workspace can set it.
     HIP_TRY(hipStreamSynchronize(nullptr));
     return EBH_OK;
 }
@@ -322,7 +337,6 @@ int ensure_host_staging(ebh_model* m, HostSlot& hs, int64_t T, int64_t outn) {
         HIP_TRY(hipHostMalloc((void**)&hs.out, std::max<int64_t>(outn, 1) * 4, hipHostMallocDefault));
         hs.out_cap = outn;
     }
-    if (!hs.err) HIP_TRY(hipHostMalloc((void**)&hs.err, 4, hipHostMallocDefault));
     if (!hs.done) HIP_TRY(hipEventCreateWithFlags(&hs.done, hipEventDisableTiming));
     return EBH_OK;
 }
@@ -352,8 +366,7 @@ int enqueue_kernels(ebh_model* m, const int* d_ids, const int* d_mask, int B, in
                                            eps, bf16 ? nullptr : w.X, w.X16, s));
         prof_end(m, s, pp, on);
     } else {
-        HIP_TRY(ebh::launch_pack(d_ids, d_mask, B, S, w.counts, w.cu, w.ntok, w.tok_id, w.tok_pos,
-                                 w.err, s));
+        HIP_TRY(ebh::launch_pack(d_ids, d_mask, B, S, w.counts, w.cu, w.ntok, w.tok_id, w.tok_pos, s));
         prof_begin(m, EBH_PROF_EMBED, s, pp, on);
         HIP_TRY(ebh::launch_embed_ln(w.tok_id, w.tok_pos, w.ntok, T, m->word, m->pos, m->type0,
                                      m->emb_g, m->emb_b, c.vocab_size, H, eps, bf16 ? nullptr : w.X, w.err,
@@ -521,6 +534,8 @@ hipGraphExec_t graph_for(ebh_model* m, const GraphEntry& key, hipStream_t s, Bod
         if (m->graphs.size() >= MAX_GRAPHS) {
             auto lru = std::min_element(m->graphs.begin(), m->graphs.end(),
                                         [](const GraphEntry& a, const GraphEntry& b) { return a.used < b.used; });
+            // Device-path launches of that recording may still be queued.
+            if (lru->exec && m->has_done && hipEventSynchronize(m->done) != hipSuccess) return nullptr;
             if (lru->exec) (void)hipGraphExecDestroy(lru->exec);
             m->graphs.erase(lru);
         }
@@ -552,8 +567,10 @@ hipGraphExec_t graph_for(ebh_model* m, const GraphEntry& key, hipStream_t s, Bod
 
 // One forward on stream s, ordered after the model's previous work.  hs (the
 // blocking entry points): ids / mask come from that slot's pinned staging
-// buffers, and the result (d_scores if given, else d_out) and the id-range
-// flag go back to it.
+// buffers, and the result (d_scores if given, else d_out) goes back to it.
+// The blocking entry points check every id on the host, so their forwards
+// never raise the device's id-range flag; that flag is sticky (kernels only
+// set it) and is read and cleared by ebh_synchronize alone.
 int run_forward(ebh_model* m, const int* d_ids, const int* d_mask, int B, int S, int normalize,
                 float* d_out, hipStream_t s, float* d_scores, HostSlot* hs, int64_t tokens = -1) {
     const bool host = hs != nullptr;
@@ -570,7 +587,6 @@ int run_forward(ebh_model* m, const int* d_ids, const int* d_mask, int B, int S,
         if (rc) return rc;
         if (host) {
             HIP_TRY(hipMemcpyAsync(hs->out, d_scores ? d_scores : d_out, n_out * 4, hipMemcpyDeviceToHost, st));
-            HIP_TRY(hipMemcpyAsync(hs->err, w.err, 4, hipMemcpyDeviceToHost, st));
         }
         return EBH_OK;
     };
@@ -618,7 +634,6 @@ int host_forward(ebh_model* m, int B, int S, int normalize, float* out, bool sco
             return rc;
     }
     HIP_TRY(hipEventSynchronize(hs.done));
-    if (*hs.err) return fail(EBH_ERR_RANGE, "token id out of range for vocab %d", m->cfg.vocab_size);
     memcpy(out, hs.out, n_out * 4);
     return EBH_OK;
 }
@@ -641,6 +656,63 @@ int check_dims(const ebh_model* m, int B, int S) {
 
 }  // namespace
 
+namespace ebh {
+// Validate one tensor against the a15 layout (name, rank, shape) and keep it
+// until ebh_finalize: f32 data is copied; with `keep` (a mapped file), data
+// is referenced in place in any encoding.
+int put_tensor(ebh_model* m, const char* name, const void* data, int kind, const int64_t* shape, int32_t ndim,
+               std::shared_ptr<const void> keep) {
+    if (!m || !name || !shape || (!data && ndim > 0) || ndim < 0) return fail(EBH_ERR_INVALID_ARG, "null argument");
+    if (m->finalized) return fail(EBH_ERR_STATE, "model already finalized");
+    if (kind != TENSOR_F32 && kind != TENSOR_F16 && kind != TENSOR_BF16)
+        return fail(EBH_ERR_INVALID_ARG, "unknown tensor encoding %d", kind);
+    if (kind != TENSOR_F32 && !keep) return fail(EBH_ERR_INVALID_ARG, "16-bit tensors are taken from files only");
+    for (int i = 0; i < ndim; ++i)
+        if (shape[i] < 0) return fail(EBH_ERR_SHAPE, "negative dimension for %s", name);
+    const std::string nm(name);
+    if (nm == "classifier.weight" || nm == "classifier.bias") {
+        // Cross-encoder head (from_cross_encoder_weights, src/lib.rs:385-399).
+        // The weight is taken as [H] (get_array1, src/weights.rs:47-58) or as
+        // the [1, H] a sequence-classification checkpoint stores; the bias must
+        // hold exactly one value (get_scalar, src/weights.rs:99-111).
+        int64_t n = 1;
+        for (int i = 0; i < ndim; ++i) n *= shape[i];
+        if (nm == "classifier.weight") {
+            const int64_t H = m->cfg.hidden_size;
+            const bool ok = (ndim == 1 && shape[0] == H) || (ndim == 2 && shape[0] == 1 && shape[1] == H);
+            if (!ok)
+                return fail(EBH_ERR_SHAPE, "Expected 1D tensor, got shape %s for %s (hidden size %lld)",
+                            shape_str(shape, ndim).c_str(), name, (long long)H);
+        } else if (n != 1) {
+            return fail(EBH_ERR_SHAPE, "Expected scalar, got %lld elements", (long long)n);
+        }
+    } else {
+        std::vector<int64_t> storage;
+        const std::vector<int64_t>* exp = expected_shape(m->cfg, name, storage);
+        if (!exp) return fail(EBH_ERR_NOT_FOUND, "unknown tensor %s", name);
+        if (exp->size() == 1 && ndim != 1)
+            return fail(EBH_ERR_SHAPE, "Expected 1D tensor, got shape %s for %s",
+                        shape_str(shape, ndim).c_str(), name);
+        if ((int)exp->size() != ndim || !std::equal(exp->begin(), exp->end(), shape))
+            return fail(EBH_ERR_SHAPE, "Shape error: %s has shape %s, expected %s", name,
+                        shape_str(shape, ndim).c_str(), shape_str(exp->data(), (int)exp->size()).c_str());
+    }
+    HostTensor t;
+    t.shape.assign(shape, shape + ndim);
+    t.kind = kind;
+    if (keep) {
+        t.src = data;
+        t.keep = std::move(keep);
+    } else {
+        const float* f = static_cast<const float*>(data);
+        t.own.assign(f, f + t.count());
+        t.src = t.own.data();
+    }
+    m->host[nm] = std::move(t);
+    return EBH_OK;
+}
+}  // namespace ebh
+
 // ===========================================================================
 // C ABI
 // ===========================================================================
@@ -661,45 +733,7 @@ int ebh_create(const ebh_config* cfg, ebh_model** out) {
 
 int ebh_set_tensor(ebh_model* m, const char* name, const float* data, const int64_t* shape,
                    int32_t ndim) {
-    if (!m || !name || !shape || (!data && ndim > 0)) return fail(EBH_ERR_INVALID_ARG, "null argument");
-    if (m->finalized) return fail(EBH_ERR_STATE, "model already finalized");
-    const std::string nm(name);
-    if (nm == "classifier.weight" || nm == "classifier.bias") {
-        // Cross-encoder head (from_cross_encoder_weights, src/lib.rs:385-399).
-        // The weight is taken as [H] (get_array1, src/weights.rs:47-58) or as
-        // the [1, H] a sequence-classification checkpoint stores; the bias must
-        // hold exactly one value (get_scalar, src/weights.rs:99-111).
-        int64_t n = 1;
-        for (int i = 0; i < ndim; ++i) n *= shape[i];
-        if (nm == "classifier.weight") {
-            const int64_t H = m->cfg.hidden_size;
-            const bool ok = (ndim == 1 && shape[0] == H) || (ndim == 2 && shape[0] == 1 && shape[1] == H);
-            if (!ok)
-                return fail(EBH_ERR_SHAPE, "Expected 1D tensor, got shape %s for %s (hidden size %lld)",
-                            shape_str(shape, ndim).c_str(), name, (long long)H);
-        } else if (n != 1) {
-            return fail(EBH_ERR_SHAPE, "Expected scalar, got %lld elements", (long long)n);
-        }
-        HostTensor& t = m->host[nm];
-        t.shape.assign(shape, shape + ndim);
-        t.data.assign(data, data + n);
-        return EBH_OK;
-    }
-    std::vector<int64_t> storage;
-    const std::vector<int64_t>* exp = expected_shape(m->cfg, name, storage);
-    if (!exp) return fail(EBH_ERR_NOT_FOUND, "unknown tensor %s", name);
-    if (exp->size() == 1 && ndim != 1)
-        return fail(EBH_ERR_SHAPE, "Expected 1D tensor, got shape %s for %s",
-                    shape_str(shape, ndim).c_str(), name);
-    if ((int)exp->size() != ndim || !std::equal(exp->begin(), exp->end(), shape))
-        return fail(EBH_ERR_SHAPE, "Shape error: %s has shape %s, expected %s", name,
-                    shape_str(shape, ndim).c_str(), shape_str(exp->data(), (int)exp->size()).c_str());
-    int64_t n = 1;
-    for (int i = 0; i < ndim; ++i) n *= shape[i];
-    HostTensor& t = m->host[name];
-    t.shape.assign(shape, shape + ndim);
-    t.data.assign(data, data + n);
-    return EBH_OK;
+    return ebh::put_tensor(m, name, data, ebh::TENSOR_F32, shape, ndim, nullptr);
 }
 
 int ebh_finalize(ebh_model* m, int32_t dtype) {
@@ -722,75 +756,105 @@ int ebh_finalize(ebh_model* m, int32_t dtype) {
 
     const ebh_config& c = m->cfg;
     const size_t H = c.hidden_size, I = c.intermediate_size, L = c.num_hidden_layers;
-    // Layout of the single device weight block.
+    const bool b16 = dtype == EBH_DTYPE_BF16;
+    // Layout of the single device weight block.  The four GEMM weights of a
+    // layer are held once, in the form the forward reads: fp32 for fp32
+    // models, bf16 for bf16 models; everything else is fp32.
     size_t off = 0;
     auto take = [&](size_t bytes) { size_t o = off; off += align_up(bytes); return o; };
-    struct Off { size_t wqkv, bqkv, wo, bo, ln1_g, ln1_b, w1, b1, w2, b2, ln2_g, ln2_b, wqkv16, wo16, w116, w216; };
+    const size_t wes = b16 ? 2 : 4;               // bytes per GEMM weight element
+    struct Off { size_t wqkv, bqkv, wo, bo, ln1_g, ln1_b, w1, b1, w2, b2, ln2_g, ln2_b; };
     const size_t oWord = take((size_t)c.vocab_size * H * 4), oPos = take((size_t)c.max_position_embeddings * H * 4),
                  oType = take(H * 4), oEg = take(H * 4), oEb = take(H * 4);
     std::vector<Off> lo(L);
     for (size_t l = 0; l < L; ++l) {
         Off& o = lo[l];
-        o.wqkv = take(3 * H * H * 4); o.bqkv = take(3 * H * 4);
-        o.wo = take(H * H * 4); o.bo = take(H * 4);
+        o.wqkv = take(3 * H * H * wes); o.bqkv = take(3 * H * 4);
+        o.wo = take(H * H * wes); o.bo = take(H * 4);
         o.ln1_g = take(H * 4); o.ln1_b = take(H * 4);
-        o.w1 = take(I * H * 4); o.b1 = take(I * 4);
-        o.w2 = take(H * I * 4); o.b2 = take(H * 4);
+        o.w1 = take(I * H * wes); o.b1 = take(I * 4);
+        o.w2 = take(H * I * wes); o.b2 = take(H * 4);
         o.ln2_g = take(H * 4); o.ln2_b = take(H * 4);
     }
     const size_t oClsW = has_cw ? take(H * 4) : 0, oClsB = has_cw ? take(4) : 0;
-    const size_t f32_bytes = off;
-    if (dtype == EBH_DTYPE_BF16)
-        for (size_t l = 0; l < L; ++l) {
-            Off& o = lo[l];
-            o.wqkv16 = take(3 * H * H * 2); o.wo16 = take(H * H * 2);
-            o.w116 = take(I * H * 2); o.w216 = take(H * I * 2);
-        }
-
-    std::vector<char> stage(f32_bytes, 0);
-    auto put = [&](size_t o, const std::string& name, size_t row_off = 0) {
-        const HostTensor& t = m->host.at(name);
-        memcpy(stage.data() + o + row_off, t.data.data(), t.data.size() * 4);
-    };
-    put(oWord, "embeddings.word_embeddings.weight");
-    put(oPos, "embeddings.position_embeddings.weight");
-    {   // token type row 0 only (src/lib.rs:658)
-        const HostTensor& t = m->host.at("embeddings.token_type_embeddings.weight");
-        memcpy(stage.data() + oType, t.data.data(), H * 4);
-    }
-    put(oEg, "embeddings.LayerNorm.weight");
-    put(oEb, "embeddings.LayerNorm.bias");
-    for (size_t l = 0; l < L; ++l) {
-        const std::string p = "encoder.layer." + std::to_string(l) + ".";
-        const Off& o = lo[l];
-        put(o.wqkv, p + "attention.self.query.weight", 0);
-        put(o.wqkv, p + "attention.self.key.weight", H * H * 4);
-        put(o.wqkv, p + "attention.self.value.weight", 2 * H * H * 4);
-        put(o.bqkv, p + "attention.self.query.bias", 0);
-        put(o.bqkv, p + "attention.self.key.bias", H * 4);
-        put(o.bqkv, p + "attention.self.value.bias", 2 * H * 4);
-        put(o.wo, p + "attention.output.dense.weight");
-        put(o.bo, p + "attention.output.dense.bias");
-        put(o.ln1_g, p + "attention.output.LayerNorm.weight");
-        put(o.ln1_b, p + "attention.output.LayerNorm.bias");
-        put(o.w1, p + "intermediate.dense.weight");
-        put(o.b1, p + "intermediate.dense.bias");
-        put(o.w2, p + "output.dense.weight");
-        put(o.b2, p + "output.dense.bias");
-        put(o.ln2_g, p + "output.LayerNorm.weight");
-        put(o.ln2_b, p + "output.LayerNorm.bias");
-    }
-    if (has_cw) {
-        put(oClsW, "classifier.weight");
-        put(oClsB, "classifier.bias");
-    }
 
     HIP_TRY(hipGetDevice(&m->device));
     HIP_TRY(hipStreamCreateWithFlags(&m->stream, hipStreamNonBlocking));
     HIP_TRY(hipEventCreateWithFlags(&m->done, hipEventDisableTiming));
     HIP_TRY(hipMalloc(&m->wbase, off));
-    HIP_TRY(hipMemcpy(m->wbase, stage.data(), f32_bytes, hipMemcpyHostToDevice));
     char* b = static_cast<char*>(m->wbase);
+
+    // Upload.  Every tensor goes from its host memory (the caller's copy, or
+    // the mapped checkpoint file) straight to its place in the block when the
+    // encodings agree (F32 -> fp32, BF16 -> bf16 GEMM weights); otherwise its
+    // bytes land in a device scratch buffer and a conversion kernel writes
+    // the destination (F16 / BF16 -> fp32 exactly; F16 / F32 -> bf16 with
+    // round to nearest even).  All copies and kernels run in order on the
+    // model's stream, so the scratch buffer is reused safely.
+    size_t scratch_bytes = 0;
+    for (auto& kv : m->host) scratch_bytes = std::max(scratch_bytes, (size_t)kv.second.count() * 4);
+    void* scratch = nullptr;
+    HIP_TRY(hipMalloc(&scratch, std::max<size_t>(scratch_bytes, 4)));
+    std::unique_ptr<void, hipError_t (*)(void*)> scratch_guard(scratch, hipFree);
+    hipStream_t st = m->stream;
+    // Elements [first, first + n) of tensor `name` (n < 0: all of it) to the
+    // block at byte offset o, as fp32 or (to16) bf16.
+    auto upload = [&](size_t o, const std::string& name, bool to16, int64_t first = 0, int64_t n = -1) -> int {
+        const HostTensor& t = m->host.at(name);
+        if (n < 0) n = t.count() - first;
+        const size_t esz = t.kind == ebh::TENSOR_F32 ? 4 : 2;
+        const char* src = static_cast<const char*>(t.src) + (size_t)first * esz;
+        void* dst = b + o;
+        const bool direct = (t.kind == ebh::TENSOR_F32 && !to16) || (t.kind == ebh::TENSOR_BF16 && to16);
+        if (direct) {
+            HIP_TRY(hipMemcpyAsync(dst, src, (size_t)n * esz, hipMemcpyHostToDevice, st));
+            return EBH_OK;
+        }
+        HIP_TRY(hipMemcpyAsync(scratch, src, (size_t)n * esz, hipMemcpyHostToDevice, st));
+        if (t.kind == ebh::TENSOR_F32)
+            HIP_TRY(ebh::launch_f32_to_bf16(static_cast<const float*>(scratch), static_cast<uint16_t*>(dst), n, st));
+        else
+            HIP_TRY(ebh::launch_widen16(static_cast<const uint16_t*>(scratch), dst, n,
+                                        t.kind == ebh::TENSOR_BF16 ? ebh::WIDEN_BF16_F32
+                                                                   : (to16 ? ebh::WIDEN_F16_BF16 : ebh::WIDEN_F16_F32),
+                                        st));
+        return EBH_OK;
+    };
+    int rc;
+#define EBH_UP(...) \
+    if ((rc = upload(__VA_ARGS__))) return rc
+    EBH_UP(oWord, "embeddings.word_embeddings.weight", false);
+    EBH_UP(oPos, "embeddings.position_embeddings.weight", false);
+    EBH_UP(oType, "embeddings.token_type_embeddings.weight", false, 0, (int64_t)H);  // row 0 only (src/lib.rs:658)
+    EBH_UP(oEg, "embeddings.LayerNorm.weight", false);
+    EBH_UP(oEb, "embeddings.LayerNorm.bias", false);
+    for (size_t l = 0; l < L; ++l) {
+        const std::string p = "encoder.layer." + std::to_string(l) + ".";
+        const Off& o = lo[l];
+        EBH_UP(o.wqkv, p + "attention.self.query.weight", b16);
+        EBH_UP(o.wqkv + H * H * wes, p + "attention.self.key.weight", b16);
+        EBH_UP(o.wqkv + 2 * H * H * wes, p + "attention.self.value.weight", b16);
+        EBH_UP(o.bqkv, p + "attention.self.query.bias", false);
+        EBH_UP(o.bqkv + H * 4, p + "attention.self.key.bias", false);
+        EBH_UP(o.bqkv + 2 * H * 4, p + "attention.self.value.bias", false);
+        EBH_UP(o.wo, p + "attention.output.dense.weight", b16);
+        EBH_UP(o.bo, p + "attention.output.dense.bias", false);
+        EBH_UP(o.ln1_g, p + "attention.output.LayerNorm.weight", false);
+        EBH_UP(o.ln1_b, p + "attention.output.LayerNorm.bias", false);
+        EBH_UP(o.w1, p + "intermediate.dense.weight", b16);
+        EBH_UP(o.b1, p + "intermediate.dense.bias", false);
+        EBH_UP(o.w2, p + "output.dense.weight", b16);
+        EBH_UP(o.b2, p + "output.dense.bias", false);
+        EBH_UP(o.ln2_g, p + "output.LayerNorm.weight", false);
+        EBH_UP(o.ln2_b, p + "output.LayerNorm.bias", false);
+    }
+    if (has_cw) {
+        EBH_UP(oClsW, "classifier.weight", false);
+        EBH_UP(oClsB, "classifier.bias", false);
+    }
+#undef EBH_UP
+    HIP_TRY(hipStreamSynchronize(st));
+
     m->word = (float*)(b + oWord);
     m->pos = (float*)(b + oPos);
     m->type0 = (float*)(b + oType);
@@ -803,32 +867,29 @@ int ebh_finalize(ebh_model* m, int32_t dtype) {
     for (size_t l = 0; l < L; ++l) {
         const Off& o = lo[l];
         DevLayer& d = m->layers[l];
-        d.wqkv = (float*)(b + o.wqkv); d.bqkv = (float*)(b + o.bqkv);
-        d.wo = (float*)(b + o.wo); d.bo = (float*)(b + o.bo);
+        d.bqkv = (float*)(b + o.bqkv); d.bo = (float*)(b + o.bo);
         d.ln1_g = (float*)(b + o.ln1_g); d.ln1_b = (float*)(b + o.ln1_b);
-        d.w1 = (float*)(b + o.w1); d.b1 = (float*)(b + o.b1);
-        d.w2 = (float*)(b + o.w2); d.b2 = (float*)(b + o.b2);
+        d.b1 = (float*)(b + o.b1); d.b2 = (float*)(b + o.b2);
         d.ln2_g = (float*)(b + o.ln2_g); d.ln2_b = (float*)(b + o.ln2_b);
+        d.wqkv = d.wo = d.w1 = d.w2 = nullptr;
         d.wqkv16 = d.wo16 = d.w116 = d.w216 = nullptr;
-        if (dtype == EBH_DTYPE_BF16) {
-            d.wqkv16 = (uint16_t*)(b + o.wqkv16); d.wo16 = (uint16_t*)(b + o.wo16);
-            d.w116 = (uint16_t*)(b + o.w116); d.w216 = (uint16_t*)(b + o.w216);
-            HIP_TRY(ebh::launch_f32_to_bf16(d.wqkv, d.wqkv16, (int64_t)(3 * H * H), m->stream));
-            HIP_TRY(ebh::launch_f32_to_bf16(d.wo, d.wo16, (int64_t)(H * H), m->stream));
-            HIP_TRY(ebh::launch_f32_to_bf16(d.w1, d.w116, (int64_t)(I * H), m->stream));
-            HIP_TRY(ebh::launch_f32_to_bf16(d.w2, d.w216, (int64_t)(H * I), m->stream));
+        if (b16) {
+            d.wqkv16 = (uint16_t*)(b + o.wqkv); d.wo16 = (uint16_t*)(b + o.wo);
+            d.w116 = (uint16_t*)(b + o.w1); d.w216 = (uint16_t*)(b + o.w2);
+        } else {
+            d.wqkv = (float*)(b + o.wqkv); d.wo = (float*)(b + o.wo);
+            d.w1 = (float*)(b + o.w1); d.w2 = (float*)(b + o.w2);
         }
     }
-    HIP_TRY(hipStreamSynchronize(m->stream));
     m->dtype = dtype;
     m->finalized = true;
-    m->host.clear();  // weights now live in HBM only
+    m->host.clear();  // weights now live in HBM only (and any mapped file is released)
     return EBH_OK;
 }
 
 void ebh_destroy(ebh_model* m) {
     if (!m) return;
-    if (m->finalized) {
+    if (m->device >= 0) {   // also after a failed ebh_finalize that got as far as the device
         (void)hipSetDevice(m->device);
         if (m->stream) (void)hipStreamSynchronize(m->stream);
         for (auto& p : m->prof_events) { (void)hipEventDestroy(p.a); (void)hipEventDestroy(p.b); }
@@ -840,7 +901,6 @@ void ebh_destroy(ebh_model* m) {
             if (hs.ids) (void)hipHostFree(hs.ids);
             if (hs.mask) (void)hipHostFree(hs.mask);
             if (hs.out) (void)hipHostFree(hs.out);
-            if (hs.err) (void)hipHostFree(hs.err);
             if (hs.done) (void)hipEventDestroy(hs.done);
         }
         if (m->done) (void)hipEventDestroy(m->done);
@@ -925,9 +985,11 @@ int ebh_encode_device(ebh_model* m, const int32_t* ids, const int32_t* mask, int
     std::lock_guard<std::mutex> lk(m->mu);
     HIP_TRY(hipSetDevice(m->device));
     hipStream_t s = stream ? static_cast<hipStream_t>(stream) : m->stream;
-    if (S == 0) {
+    if (S == 0) {   // mean over an empty sequence: zero rows, ordered like a forward
         if (m->has_done) HIP_TRY(hipStreamWaitEvent(s, m->done, 0));
-        HIP_TRY(hipMemsetAsync(out, 0, sizeof(float) * (size_t)B * m->cfg.hidden_size, s));
+        HIP_TRY(ebh::launch_zero_words(out, (int64_t)B * m->cfg.hidden_size, s));
+        HIP_TRY(hipEventRecord(m->done, s));
+        m->has_done = true;
         return EBH_OK;
     }
     if ((rc = ensure_workspace(m, B, S))) return rc;
@@ -1279,8 +1341,9 @@ int ebh_op_pack(const int32_t* ids, const int32_t* mask, int32_t B, int32_t S, i
     if (!ids || !mask || !counts || !cu_seqlens || !n_tokens || !tok_id || !tok_pos || !err)
         return fail(EBH_ERR_INVALID_ARG, "null buffer");
     if (B < 0 || S < 0) return fail(EBH_ERR_INVALID_ARG, "bad pack shape");
-    HIP_TRY(ebh::launch_pack(ids, mask, B, S, counts, cu_seqlens, n_tokens, tok_id, tok_pos, err,
+    HIP_TRY(ebh::launch_pack(ids, mask, B, S, counts, cu_seqlens, n_tokens, tok_id, tok_pos,
                              static_cast<hipStream_t>(stream)));
+    HIP_TRY(ebh::launch_zero_words(err, 1, static_cast<hipStream_t>(stream)));
     return EBH_OK;
 }
 
@@ -1299,6 +1362,19 @@ int ebh_op_embed_ln(const int32_t* tok_id, const int32_t* tok_pos, const int32_t
 int ebh_op_f32_to_bf16(const float* x, uint16_t* y, int64_t n, void* stream) {
     if (!x || !y || n < 0) return fail(EBH_ERR_INVALID_ARG, "bad conversion arguments");
     HIP_TRY(ebh::launch_f32_to_bf16(x, y, n, static_cast<hipStream_t>(stream)));
+    return EBH_OK;
+}
+
+int ebh_op_widen16(const uint16_t* x, void* y, int64_t n, int32_t mode, void* stream) {
+    if (!x || !y || n < 0 || mode < ebh::WIDEN_F16_F32 || mode > ebh::WIDEN_F16_BF16)
+        return fail(EBH_ERR_INVALID_ARG, "bad conversion arguments");
+    HIP_TRY(ebh::launch_widen16(x, y, n, mode, static_cast<hipStream_t>(stream)));
+    return EBH_OK;
+}
+
+int ebh_op_gelu(const float* x, float* y, int64_t n, void* stream) {
+    if (!x || !y || n < 0) return fail(EBH_ERR_INVALID_ARG, "bad GELU arguments");
+    HIP_TRY(ebh::launch_gelu(x, y, n, static_cast<hipStream_t>(stream)));
     return EBH_OK;
 }
 

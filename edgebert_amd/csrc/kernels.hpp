@@ -97,7 +97,10 @@ hipError_t launch_add_layernorm_y16(const uint16_t* y, const float* bias, float*
 
 // Token packing: mask [B,S] -> cu_seqlens [B+1], n_tokens, packed ids/positions.
 hipError_t launch_pack(const int* ids, const int* mask, int B, int S, int* counts, int* cu,
-                       int* n_tokens, int* tok_id, int* tok_pos, int* err, hipStream_t s);
+                       int* n_tokens, int* tok_id, int* tok_pos, hipStream_t s);
+
+// n 32-bit words at p set to zero (a kernel launch, never a memset node).
+hipError_t launch_zero_words(void* p, int64_t n, hipStream_t s);
 
 // Packing and embeddings in one launch for B*S <= 64 positions (the float4 row
 // shapes): the same outputs as launch_pack followed by launch_embed_ln.
@@ -128,6 +131,15 @@ hipError_t launch_cls_head(const float* pooled, const float* w, const float* bia
 // fp32 -> bf16 (round to nearest even) for weight upload.
 hipError_t launch_f32_to_bf16(const float* x, uint16_t* y, int64_t n, hipStream_t s);
 
+// y = the fused epilogues' tanh-form GELU of x, elementwise (op-level check
+// of its error bound).
+hipError_t launch_gelu(const float* x, float* y, int64_t n, hipStream_t s);
+
+// Half-precision checkpoint tensors (safetensors F16 / BF16) to device form:
+// F16 -> f32 and BF16 -> f32 exactly, F16 -> bf16 rounded to nearest even.
+enum Widen16 : int { WIDEN_F16_F32 = 0, WIDEN_BF16_F32 = 1, WIDEN_F16_BF16 = 2 };
+hipError_t launch_widen16(const uint16_t* x, void* y, int64_t n, int mode, hipStream_t s);
+
 // ---------------------------------------------------------------------------
 // device helpers
 // ---------------------------------------------------------------------------
@@ -143,7 +155,14 @@ __device__ __forceinline__ float wave_max(float v) {
     return v;
 }
 
-// exp(x) = 2^(x * log2 e) on the hardware exp2 (v_exp_f32).
+// exp(x) = 2^(x * log2 e) on the hardware exp2 (v_exp_f32).  The rounded
+// product x log2(e) has relative error <= 2 eps (eps = 2^-24: the constant
+// and the product), which exp2 turns into |x| 2 eps relative error of the
+// result, plus its own 1 ulp: |fast_exp(x) - e^x| <= (2 |x| + 2) eps e^x.
+// The softmax calls it with x = score - row max <= 0, so each unnormalised
+// probability is off by at most max over x <= 0 of (2|x| + 2) eps e^x = 2 eps
+// absolute (1.2e-7).  Below x = -87.3 the result is 0 (flushed), against a
+// true value below 1.2e-38.
 __device__ __forceinline__ float fast_exp(float x) {
     return __builtin_amdgcn_exp2f(x * 1.4426950408889634f);
 }

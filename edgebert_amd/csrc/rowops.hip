@@ -5,6 +5,8 @@
 // element c*64 + lane so every load/store instruction covers 256 contiguous
 // bytes); mean and variance are two wave reductions over register-resident
 // values, so each row is read once and written once.
+#include <algorithm>
+
 #include "kernels.hpp"
 
 namespace ebh {
@@ -17,8 +19,7 @@ namespace ebh {
 // positions for the position embedding.
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(256) void pack_count_kernel(const int* __restrict__ mask, int S,
-                                                         int* __restrict__ counts,
-                                                         int* __restrict__ err) {
+                                                         int* __restrict__ counts) {
     __shared__ int part[4];
     const int b = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     int n = 0;
@@ -30,10 +31,7 @@ __global__ __launch_bounds__(256) void pack_count_kernel(const int* __restrict__
     }
     if (lane == 0) part[wave] = n;
     __syncthreads();
-    if (tid == 0) {
-        counts[b] = part[0] + part[1] + part[2] + part[3];
-        if (b == 0) *err = 0;  // clear the id-range flag for this forward
-    }
+    if (tid == 0) counts[b] = part[0] + part[1] + part[2] + part[3];
 }
 
 // Exclusive scan of counts[0..B) -> cu[0..B], n_tokens = cu[B]; one workgroup.
@@ -94,12 +92,25 @@ __global__ __launch_bounds__(256) void pack_scatter_kernel(const int* __restrict
 }
 
 hipError_t launch_pack(const int* ids, const int* mask, int B, int S, int* counts, int* cu,
-                       int* n_tokens, int* tok_id, int* tok_pos, int* err, hipStream_t s) {
+                       int* n_tokens, int* tok_id, int* tok_pos, hipStream_t s) {
     if (B <= 0) return hipSuccess;
-    hipLaunchKernelGGL(pack_count_kernel, dim3(B), dim3(256), 0, s, mask, S, counts, err);
+    hipLaunchKernelGGL(pack_count_kernel, dim3(B), dim3(256), 0, s, mask, S, counts);
     hipLaunchKernelGGL(pack_scan_kernel, dim3(1), dim3(1024), 0, s, counts, B, cu, n_tokens);
     hipLaunchKernelGGL(pack_scatter_kernel, dim3(B), dim3(256), 0, s, ids, mask, S, cu, tok_id,
                        tok_pos);
+    return hipGetLastError();
+}
+
+// n 32-bit words of p set to 0: a kernel, not hipMemsetAsync, so that a caller
+// capturing its stream into a HIP graph records a kernel node.
+__global__ __launch_bounds__(256) void zero_words_kernel(uint32_t* __restrict__ p, int64_t n) {
+    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) p[i] = 0u;
+}
+
+hipError_t launch_zero_words(void* p, int64_t n, hipStream_t s) {
+    if (n <= 0) return hipSuccess;
+    const int64_t blocks = std::min<int64_t>((n + 255) / 256, 1024);
+    hipLaunchKernelGGL(zero_words_kernel, dim3((unsigned)blocks), dim3(256), 0, s, static_cast<uint32_t*>(p), n);
     return hipGetLastError();
 }
 
@@ -676,7 +687,7 @@ __global__ __launch_bounds__(256) void pack_embed_few_kernel(
         if (lane == 0) {
             cu[B] = n;
             *n_tokens = n;
-            *err = bad != 0ull;
+            if (bad) *err = 1;                    // sticky: only ebh_synchronize clears it
         }
     }
     constexpr int RPB = 256 / LPR;
@@ -950,6 +961,50 @@ hipError_t launch_f32_to_bf16(const float* x, uint16_t* y, int64_t n, hipStream_
     const int64_t blocks = (n + 255) / 256;
     hipLaunchKernelGGL(f32_to_bf16_kernel, dim3((unsigned)(blocks < 65536 ? blocks : 65536)),
                        dim3(256), 0, s, x, y, n);
+    return hipGetLastError();
+}
+
+// IEEE binary16 bits -> the float of the same value, exactly: a normal f16
+// rebiases its exponent (15 -> 127); a subnormal m * 2^-24 (m < 1024) is
+// normalised (shifted until bit 10 is set, the exponent counting down); zero
+// keeps its sign; inf and NaN keep the all-ones exponent and the mantissa
+// bits (NaN payloads shifted up, as a hardware widening does for quiet NaNs).
+__device__ __forceinline__ float f16_bits_to_f32(uint32_t h) {
+    const uint32_t sign = (h & 0x8000u) << 16;
+    uint32_t exp = (h >> 10) & 0x1Fu, man = h & 0x3FFu;
+    if (exp == 0x1Fu) return __uint_as_float(sign | 0x7F800000u | (man << 13));
+    if (exp == 0) {
+        if (man == 0) return __uint_as_float(sign);
+        const int lz = __clz(man) - 21;           // zeros above bit 10 of man (1..10)
+        man = (man << lz) & 0x3FFu;
+        exp = 1 - lz;                             // f16 exponent of the normalised value
+    }
+    return __uint_as_float(sign | ((exp + 112u) << 23) | (man << 13));
+}
+
+// 16-bit checkpoint tensors to their device form: F16 or BF16 bits -> f32
+// (exact), or F16 bits -> bf16 (the exact f32 value rounded to nearest even).
+// BF16 bits need no kernel for a bf16 destination.
+template <int MODE>   // 0: f16 -> f32, 1: bf16 -> f32, 2: f16 -> bf16
+__global__ __launch_bounds__(256) void widen16_kernel(const uint16_t* __restrict__ x, void* __restrict__ y,
+                                                      int64_t n) {
+    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) {
+        const uint32_t h = x[i];
+        if constexpr (MODE == 0) static_cast<float*>(y)[i] = f16_bits_to_f32(h);
+        if constexpr (MODE == 1) static_cast<float*>(y)[i] = __uint_as_float(h << 16);
+        if constexpr (MODE == 2) static_cast<uint16_t*>(y)[i] = f32_to_bf16_rne(f16_bits_to_f32(h));
+    }
+}
+
+hipError_t launch_widen16(const uint16_t* x, void* y, int64_t n, int mode, hipStream_t s) {
+    if (n <= 0) return hipSuccess;
+    const dim3 grid((unsigned)std::min<int64_t>((n + 255) / 256, 65536)), block(256);
+    switch (mode) {
+        case WIDEN_F16_F32: hipLaunchKernelGGL(widen16_kernel<0>, grid, block, 0, s, x, y, n); break;
+        case WIDEN_BF16_F32: hipLaunchKernelGGL(widen16_kernel<1>, grid, block, 0, s, x, y, n); break;
+        case WIDEN_F16_BF16: hipLaunchKernelGGL(widen16_kernel<2>, grid, block, 0, s, x, y, n); break;
+        default: return hipErrorInvalidValue;
+    }
     return hipGetLastError();
 }
 

@@ -5,9 +5,19 @@
 // name to {"dtype", "shape", "data_offsets": [begin, end]} (offsets relative
 // to the end of the header), optional "__metadata__", then the raw data.
 // The reference decodes every tensor as f32 LE whatever its dtype
-// (src/weights.rs:25-29); here F32 is taken as-is and F16 / BF16 are widened
-// exactly, any other dtype of a tensor the encoder needs is an error, and
-// tensors the encoder does not use are skipped.
+// (src/weights.rs:25-29).  Here the file is mapped, each tensor the encoder
+// needs is handed to the model as a view of its bytes in the mapping (F32,
+// F16 or BF16), and ebh_finalize uploads it from there in that encoding: no
+// host copy, 16-bit tensors cross PCIe at 16 bits and are converted on the
+// device (BF16 GEMM weights of bf16 models not at all).  Any other dtype of a
+// needed tensor is an error; tensors the encoder does not use are skipped.
+// The mapping is released at ebh_finalize or ebh_destroy, so the file must
+// not be truncated before then.
+#include <fcntl.h>
+#include <sys/mman.h>
+#include <sys/stat.h>
+#include <unistd.h>
+
 #include <cstdint>
 #include <cstdio>
 #include <cstring>
@@ -25,71 +35,65 @@ namespace {
 using ebh::json::JVal;
 using ebh::json::Parser;
 
+int fail(int code, const std::string& msg) { return ebh::set_error(code, "%s", msg.c_str()); }
 
-float half_to_float(uint16_t h) {
-    const uint32_t sign = (uint32_t)(h & 0x8000u) << 16;
-    uint32_t exp = (h >> 10) & 0x1Fu, man = h & 0x3FFu, bits;
-    if (exp == 0) {
-        if (man == 0) {
-            bits = sign;
-        } else {  // subnormal: renormalise
-            exp = 127 - 15 + 1;
-            while (!(man & 0x400u)) { man <<= 1; --exp; }
-            bits = sign | (exp << 23) | ((man & 0x3FFu) << 13);
-        }
-    } else if (exp == 0x1F) {
-        bits = sign | 0x7F800000u | (man << 13);
-    } else {
-        bits = sign | ((exp + 127 - 15) << 23) | (man << 13);
+// A read-only private mapping of the whole file, unmapped with its last owner.
+std::shared_ptr<const void> map_file(const char* path, size_t* size, std::string* err) {
+    const int fd = open(path, O_RDONLY | O_CLOEXEC);
+    if (fd < 0) {
+        *err = std::string("cannot open ") + path;
+        return nullptr;
     }
-    float f;
-    memcpy(&f, &bits, 4);
-    return f;
+    struct stat sb;
+    if (fstat(fd, &sb) != 0 || !S_ISREG(sb.st_mode)) {
+        close(fd);
+        *err = std::string("cannot open ") + path + " (not a regular file)";
+        return nullptr;
+    }
+    *size = (size_t)sb.st_size;
+    if (*size < 8) {
+        close(fd);
+        *err = "safetensors: truncated header";
+        return nullptr;
+    }
+    void* p = mmap(nullptr, *size, PROT_READ, MAP_PRIVATE, fd, 0);
+    close(fd);
+    if (p == MAP_FAILED) {
+        *err = std::string("cannot map ") + path;
+        return nullptr;
+    }
+    const size_t n = *size;
+    return std::shared_ptr<const void>(p, [n](const void* q) { munmap(const_cast<void*>(q), n); });
 }
-
-float bf16_to_float(uint16_t h) {
-    uint32_t bits = (uint32_t)h << 16;
-    float f;
-    memcpy(&f, &bits, 4);
-    return f;
-}
-
-int fail(int code, const char* msg) { return ebh::set_error(code, "%s", msg); }
 
 }  // namespace
 
 extern "C" int ebh_load_safetensors(ebh_model* m, const char* path) {
     if (!m || !path) return fail(EBH_ERR_INVALID_ARG, "null argument");
-    std::unique_ptr<FILE, int (*)(FILE*)> f(fopen(path, "rb"), fclose);
-    if (!f) return fail(EBH_ERR_NOT_FOUND, (std::string("cannot open ") + path).c_str());
-    uint8_t lenb[8];
-    if (fread(lenb, 1, 8, f.get()) != 8) return fail(EBH_ERR_SHAPE, "safetensors: truncated header");
+    size_t fsize = 0;
+    std::string err;
+    std::shared_ptr<const void> map = map_file(path, &fsize, &err);
+    if (!map) return fail(err.rfind("cannot", 0) == 0 ? EBH_ERR_NOT_FOUND : EBH_ERR_SHAPE, err);
+    const uint8_t* bytes = static_cast<const uint8_t*>(map.get());
     uint64_t n = 0;
-    for (int i = 7; i >= 0; --i) n = (n << 8) | lenb[i];
+    for (int i = 7; i >= 0; --i) n = (n << 8) | bytes[i];
     if (n > (100u << 20)) return fail(EBH_ERR_SHAPE, "safetensors: header too large");
-    std::string header(n, '\0');
-    if (fread(&header[0], 1, n, f.get()) != n) return fail(EBH_ERR_SHAPE, "safetensors: truncated header");
-    if (fseek(f.get(), 0, SEEK_END) != 0) return fail(EBH_ERR_SHAPE, "safetensors: seek failed");
-    const long fsize = ftell(f.get());
+    if (n > fsize - 8) return fail(EBH_ERR_SHAPE, "safetensors: truncated header");
     const uint64_t data_start = 8 + n;
-    if (fsize < 0 || (uint64_t)fsize < data_start) return fail(EBH_ERR_SHAPE, "safetensors: truncated file");
     const uint64_t data_len = (uint64_t)fsize - data_start;
+    const char* header = reinterpret_cast<const char*>(bytes + 8);
 
-    Parser ps{header.data(), header.data() + header.size(), {}};
+    Parser ps{header, header + n, {}};
     JVal root;
     if (!ps.parse(root) || root.kind != JVal::OBJ)
-        return fail(EBH_ERR_SHAPE, ("safetensors: bad header JSON: " + ps.err).c_str());
+        return fail(EBH_ERR_SHAPE, "safetensors: bad header JSON: " + ps.err);
 
-    ebh_config cfg;
-    ebh_model_info(m, &cfg, nullptr);
-    std::vector<float> buf;
-    std::vector<uint8_t> raw;
     for (auto& kv : root.obj) {
         const std::string& name = kv.first;
         if (name == "__metadata__") continue;
         const JVal& t = kv.second;
         if (t.kind != JVal::OBJ || !t.obj.count("dtype") || !t.obj.count("shape") || !t.obj.count("data_offsets"))
-            return fail(EBH_ERR_SHAPE, ("safetensors: malformed entry " + name).c_str());
+            return fail(EBH_ERR_SHAPE, "safetensors: malformed entry " + name);
         // The encoder's tensors and the cross-encoder head; pooler / position_ids are skipped.
         const bool wanted = name.rfind("embeddings.", 0) == 0 || name.rfind("encoder.layer.", 0) == 0 ||
                             name == "classifier.weight" || name == "classifier.bias";
@@ -98,7 +102,7 @@ extern "C" int ebh_load_safetensors(ebh_model* m, const char* path) {
         const JVal& shp = t.obj.at("shape");
         const JVal& offs = t.obj.at("data_offsets");
         if (shp.kind != JVal::ARR || offs.kind != JVal::ARR || offs.arr.size() != 2)
-            return fail(EBH_ERR_SHAPE, ("safetensors: malformed entry " + name).c_str());
+            return fail(EBH_ERR_SHAPE, "safetensors: malformed entry " + name);
         std::vector<int64_t> shape;
         uint64_t count = 1;
         for (auto& d : shp.arr) {
@@ -106,35 +110,25 @@ extern "C" int ebh_load_safetensors(ebh_model* m, const char* path) {
             // count of any tensor this model could hold.
             if (d.kind != JVal::NUM || !(d.num >= 0.0) || d.num != (double)(int64_t)d.num ||
                 d.num > (double)(1ull << 40))
-                return fail(EBH_ERR_SHAPE, ("safetensors: bad shape for " + name).c_str());
+                return fail(EBH_ERR_SHAPE, "safetensors: bad shape for " + name);
             shape.push_back((int64_t)d.num);
             count *= (uint64_t)d.num;
-            if (count > (1ull << 40))
-                return fail(EBH_ERR_SHAPE, ("safetensors: bad shape for " + name).c_str());
+            if (count > (1ull << 40)) return fail(EBH_ERR_SHAPE, "safetensors: bad shape for " + name);
         }
         for (auto& o : offs.arr)
             if (o.kind != JVal::NUM || !(o.num >= 0.0) || o.num > 9.0e15)
-                return fail(EBH_ERR_SHAPE, ("safetensors: bad data_offsets for " + name).c_str());
+                return fail(EBH_ERR_SHAPE, "safetensors: bad data_offsets for " + name);
         const uint64_t b0 = (uint64_t)offs.arr[0].num, b1 = (uint64_t)offs.arr[1].num;
-        const int esz = dt == "F32" ? 4 : (dt == "F16" || dt == "BF16") ? 2 : 0;
-        if (!esz)
-            return fail(EBH_ERR_SHAPE, ("safetensors: unsupported dtype " + dt + " for " + name).c_str());
+        // The reference reads every tensor as f32 LE (src/weights.rs:25-29);
+        // here F16 and BF16 stay 16-bit until the device converts them.
+        const int kind = dt == "F32" ? ebh::TENSOR_F32 : dt == "F16" ? ebh::TENSOR_F16
+                       : dt == "BF16" ? ebh::TENSOR_BF16 : -1;
+        if (kind < 0) return fail(EBH_ERR_SHAPE, "safetensors: unsupported dtype " + dt + " for " + name);
+        const uint64_t esz = kind == ebh::TENSOR_F32 ? 4 : 2;
         if (b1 < b0 || b1 > data_len || b1 - b0 != count * esz)
-            return fail(EBH_ERR_SHAPE, ("safetensors: bad data_offsets for " + name).c_str());
-        raw.resize(b1 - b0);
-        if (fseek(f.get(), (long)(data_start + b0), SEEK_SET) != 0 ||
-            fread(raw.data(), 1, raw.size(), f.get()) != raw.size())
-            return fail(EBH_ERR_SHAPE, ("safetensors: read failed for " + name).c_str());
-        buf.resize(count);
-        if (esz == 4) {
-            memcpy(buf.data(), raw.data(), raw.size());  // little-endian host
-        } else {
-            for (uint64_t i = 0; i < count; ++i) {
-                const uint16_t h = (uint16_t)(raw[2 * i] | (raw[2 * i + 1] << 8));
-                buf[i] = dt == "F16" ? half_to_float(h) : bf16_to_float(h);
-            }
-        }
-        const int rc = ebh_set_tensor(m, name.c_str(), buf.data(), shape.data(), (int32_t)shape.size());
+            return fail(EBH_ERR_SHAPE, "safetensors: bad data_offsets for " + name);
+        const int rc = ebh::put_tensor(m, name.c_str(), bytes + data_start + b0, kind, shape.data(),
+                                       (int32_t)shape.size(), map);
         if (rc) return rc;
     }
     return EBH_OK;

@@ -82,7 +82,12 @@ EBH_API int ebh_set_tensor(ebh_model* m, const char* name, const float* data, co
                    int32_t ndim);
 
 /* Load every tensor from a model.safetensors file (src/weights.rs:15-45).
- * F32 tensors are read as-is; F16 and BF16 are widened to f32.  A
+ * F32, F16 and BF16 tensors are taken in their own encoding: the file is
+ * mapped, and ebh_finalize uploads each tensor straight from the mapping
+ * (F32 into fp32 slots; BF16 GEMM weights straight into a bf16 model's
+ * weights; anything else converted on the device: F16 / BF16 -> fp32 exactly,
+ * F16 / F32 -> bf16 rounded to nearest even).  The file must stay unchanged
+ * until ebh_finalize or ebh_destroy releases the mapping.  A
  * classifier.weight / classifier.bias pair is loaded as the cross-encoder
  * head; other tensors the encoder does not use (pooler.*) are skipped. */
 EBH_API int ebh_load_safetensors(ebh_model* m, const char* path);
@@ -90,8 +95,9 @@ EBH_API int ebh_load_safetensors(ebh_model* m, const char* path);
 /* End of from_weights: check that every tensor is present (missing ->
  * EBH_ERR_NOT_FOUND "Tensor <name> not found"), bind the model to the
  * current HIP device, upload all weights once into
- * one device-resident HBM block (QKV concatenated to [3H, H]) and, for
- * EBH_DTYPE_BF16, keep bf16 copies of the GEMM weights. */
+ * one device-resident HBM block (QKV concatenated to [3H, H]).  With
+ * EBH_DTYPE_BF16 the four GEMM weights of each layer are held as bf16 only
+ * (round to nearest even from F32 / F16, as-is from BF16). */
 EBH_API int ebh_finalize(ebh_model* m, int32_t dtype);
 
 EBH_API void ebh_destroy(ebh_model* m);
@@ -118,7 +124,9 @@ EBH_API int ebh_encode(ebh_model* m, const uint32_t* ids, const uint32_t* mask, 
  * device pointers; enqueued on `stream` (a hipStream_t, NULL = the model's own
  * stream) and returns without waiting.  Ids are range-checked on the device:
  * an id >= vocab_size reads row 0 and is reported by the next
- * ebh_synchronize().  Successive calls are ordered even across streams. */
+ * ebh_synchronize(), however many forwards follow it.  Successive calls are
+ * ordered even across streams (S == 0 included: zero rows, written by a
+ * kernel).  No call enqueues a memset, so `stream` may be under capture. */
 EBH_API int ebh_encode_device(ebh_model* m, const int32_t* ids, const int32_t* mask, int32_t B,
                       int32_t S, int32_t normalize, float* out, void* stream);
 
@@ -197,7 +205,9 @@ EBH_API int ebh_score_texts(ebh_model* m, const ebh_tokenizer* t, const char* co
 EBH_API int ebh_set_graph_replay(ebh_model* m, int32_t enable);
 
 /* Wait for the model's outstanding work; EBH_ERR_RANGE if a device-side id
- * check failed since the previous ebh_synchronize / blocking call. */
+ * check of any _device forward failed since the previous ebh_synchronize.
+ * The flag is sticky: later clean forwards do not clear it, only this call
+ * does (blocking calls check their ids on the host and leave it alone). */
 EBH_API int ebh_synchronize(ebh_model* m);
 
 /* The packed token stream the last forward consumed: n_tokens (mask == 1

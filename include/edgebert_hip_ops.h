@@ -110,7 +110,8 @@ EBH_API int ebh_op_pool_b16(const uint16_t* x16, const int32_t* cu_seqlens, int3
                     int32_t normalize, float* out, void* stream);
 
 /* Token packing: ids / mask [B, S] -> cu_seqlens [B+1], n_tokens [1],
- * tok_id / tok_pos [B*S]; counts [B] is scratch; err [1] is cleared. */
+ * tok_id / tok_pos [B*S]; counts [B] is scratch; err [1] is cleared (the
+ * forward itself never clears its flag: see ebh_synchronize). */
 EBH_API int ebh_op_pack(const int32_t* ids, const int32_t* mask, int32_t B, int32_t S,
                 int32_t* counts, int32_t* cu_seqlens, int32_t* n_tokens, int32_t* tok_id,
                 int32_t* tok_pos, int32_t* err, void* stream);
@@ -125,6 +126,15 @@ EBH_API int ebh_op_embed_ln(const int32_t* tok_id, const int32_t* tok_pos, const
 
 /* fp32 -> bf16 bits, round to nearest even (weight conversion). */
 EBH_API int ebh_op_f32_to_bf16(const float* x, uint16_t* y, int64_t n, void* stream);
+
+/* The device conversion of 16-bit checkpoint tensors (ebh_load_safetensors +
+ * ebh_finalize): mode 0 F16 bits -> f32, 1 BF16 bits -> f32 (both exact,
+ * y float[n]), 2 F16 bits -> bf16 bits rounded to nearest even (y uint16[n]). */
+EBH_API int ebh_op_widen16(const uint16_t* x, void* y, int64_t n, int32_t mode, void* stream);
+
+/* The tanh-form GELU as fused into the FFN-up epilogues, elementwise:
+ * y[i] = gelu(x[i]) with the epilogue's exp2 + reciprocal evaluation. */
+EBH_API int ebh_op_gelu(const float* x, float* y, int64_t n, void* stream);
 
 #ifdef __cplusplus
 }

@@ -212,6 +212,77 @@ def test_f32_to_bf16_round_to_nearest_even(env):
     assert np.isnan(np.frombuffer((got[~fin].astype(np.uint32) << 16).tobytes(), np.float32)).all()
 
 
+def _all_16bit_patterns():
+    return np.arange(65536, dtype=np.uint32).astype(np.uint16)
+
+
+@pytest.mark.parametrize("mode", [0, 1, 2])
+def test_widen16_every_bit_pattern(env, mode):
+    """The device conversion of F16 / BF16 checkpoint tensors, on all 65536
+    bit patterns (zeros of both signs, every subnormal, +-inf, NaNs):
+    F16 -> f32 equals numpy's float16 widening, BF16 -> f32 the 16-bit shift,
+    F16 -> bf16 torch's round-to-nearest-even of that f32 value; a NaN stays a
+    NaN of the same sign."""
+    torch, eb, Nn, L = env
+    x = _all_16bit_patterns()
+    dx = dev(torch, x.view(np.int16))
+    if mode == 2:
+        dy = torch.empty(x.size, dtype=torch.int16, device="cuda")
+    else:
+        dy = torch.empty(x.size, dtype=torch.float32, device="cuda")
+    Nn.check(L.ebh_op_widen16(vp(dx), vp(dy), x.size, mode, stream(torch)))
+    torch.cuda.synchronize()
+    f16 = x.view(np.float16).astype(np.float32)
+    if mode == 0:
+        got, want = dy.cpu().numpy(), f16
+    elif mode == 1:
+        got, want = dy.cpu().numpy(), (x.astype(np.uint32) << 16).view(np.float32)
+    else:
+        got_b = dy.cpu().numpy().view(np.uint16)
+        want_b = torch.from_numpy(f16).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+        got = (got_b.astype(np.uint32) << 16).view(np.float32)
+        want = (want_b.astype(np.uint32) << 16).view(np.float32)
+    nan = np.isnan(want)
+    assert nan.sum() == (2046 if mode != 1 else 254)
+    np.testing.assert_array_equal(got[~nan].view(np.uint32), want[~nan].view(np.uint32))
+    assert np.isnan(got[nan]).all()
+    assert (np.signbit(got[nan]) == (x[nan] >= 0x8000)).all()   # torch's own bf16 NaN is unsigned
+
+
+def test_gelu_error_bound(env):
+    """The fused GELU (exp2 + reciprocal form) against the float64 tanh form of
+    the reference (src/lib.rs:958-978) over [-12, 12] in steps of 2^-12 and
+    2^20 random values, within its stated bound
+    |err| <= (8 ln2 |t| + 8) 2^-24 |gelu(x)|, t = x (K1 + K2 x^2) (plus 2e-37
+    absolute where the result leaves the normal fp32 range)."""
+    torch, eb, Nn, L = env
+    rng = np.random.default_rng(17)
+    x = np.concatenate([np.arange(-12 * 4096, 12 * 4096 + 1) / 4096.0,
+                        rng.standard_normal(1 << 20) * 3.0, [0.0, -0.0]]).astype(np.float32)
+    dx = dev(torch, x)
+    dy = torch.empty_like(dx)
+    Nn.check(L.ebh_op_gelu(vp(dx), vp(dy), x.size, stream(torch)))
+    torch.cuda.synchronize()
+    got = dy.cpu().numpy().astype(np.float64)
+    x64 = x.astype(np.float64)
+    # 0.5 (1 + tanh u) = 1 / (1 + e^(-2u)): the second form has no cancellation
+    # in float64 where tanh u -> -1 (x < -5); the two agree elsewhere.
+    u = 0.7978845608 * (x64 + 0.044715 * x64 ** 3)
+    with np.errstate(over="ignore"):
+        want = x64 / (1.0 + np.exp(-2.0 * u))
+    well = x64 > -3
+    np.testing.assert_allclose(want[well], gelu64(x64[well]), rtol=1e-13, atol=1e-300)
+    k1 = -2.0 * np.log2(np.e) * 0.7978845608
+    t = x64 * (k1 + k1 * 0.044715 * x64 * x64)
+    bound = (8 * np.log(2) * np.abs(t) + 8) * 2.0 ** -24 * np.abs(want) + 2e-37
+    err = np.abs(got - want)
+    worst = float((err / bound).max())
+    print(f"gelu: max abs err {err.max():.3e}, max err / bound {worst:.3f}, "
+          f"max rel err (x >= -5) {float((err / np.maximum(np.abs(want), 1e-30))[x64 >= -5].max()):.3e}")
+    assert worst <= 1.0
+    assert np.isfinite(got).all()
+
+
 # ---------------------------------------------------------------------------
 # attention (QK^T, scale, key-padding mask, softmax, PV) over packed sequences
 # ---------------------------------------------------------------------------
@@ -637,6 +708,69 @@ def test_device_path_reports_bad_id_on_synchronize(env, minilm):
     np.testing.assert_array_equal(out.cpu().numpy(), host)
 
 
+@pytest.mark.parametrize("B,S", [(2, 8), (4, 40)])
+def test_bad_id_flag_is_sticky_across_later_forwards(env, minilm, B, S):
+    """A bad id in one queued device forward is still reported after clean
+    forwards follow it (pipelined use), after a blocking call, and after the
+    workspace grows; ebh_synchronize reports it once and clears it.  (2, 8)
+    packs and embeds in one launch, (4, 40) in the separate kernels."""
+    torch, eb, Nn, L = env
+    s = torch.cuda.current_stream().cuda_stream
+    ids = torch.full((B, S), 101, dtype=torch.int32, device="cuda")
+    mask = torch.ones_like(ids)
+    out = torch.empty((B, 384), device="cuda")
+    bad = ids.clone()
+    bad[B - 1, 3] = 40000
+    good_host = ids.cpu().numpy().astype(np.uint32)
+    minilm.synchronize()
+    for after in ("device", "blocking", "grow"):
+        minilm.encode_device(bad.data_ptr(), mask.data_ptr(), B, S, out.data_ptr(), True, s)
+        if after == "device":
+            for _ in range(3):
+                minilm.encode_device(ids.data_ptr(), mask.data_ptr(), B, S, out.data_ptr(), True, s)
+        elif after == "blocking":
+            got = minilm.encode_ids(good_host, good_host * 0 + 1)
+            assert np.isfinite(got).all()
+        else:
+            # 160 x 300 tokens: more than any other test of this module runs
+            big = torch.full((160, 300), 101, dtype=torch.int32, device="cuda")
+            big_mask = torch.ones_like(big)
+            big_out = torch.empty((160, 384), device="cuda")
+            minilm.encode_device(big.data_ptr(), big_mask.data_ptr(), 160, 300,
+                                 big_out.data_ptr(), True, s)
+        with pytest.raises(eb.EbhError, match="out of range") as e:
+            minilm.synchronize()
+        assert e.value.code == Nn.EBH_ERR_RANGE, after
+        minilm.synchronize()                         # read once, then clear
+
+
+def test_empty_sequence_device_call_is_ordered_after_earlier_forwards(env, minilm, weights_for):
+    """S == 0 on the device path writes zero rows with a kernel, ordered after
+    the model's earlier work on another stream and before later work: a long
+    forward into `out` on stream A, then S == 0 into the same `out` on stream
+    B, leaves zeros; a forward after it leaves vectors again."""
+    torch, eb, Nn, L = env
+    spec = eb.CONFIGS["c3"]
+    ids_np, mask_np, _ = eb.make_inputs(spec)
+    ids = torch.from_numpy(ids_np.astype(np.int32)).cuda()
+    mask = torch.from_numpy(mask_np.astype(np.int32)).cuda()
+    out = torch.full((spec.batch, 384), 7.0, device="cuda")
+    sa, sb = torch.cuda.Stream(), torch.cuda.Stream()
+    torch.cuda.synchronize()
+    for _ in range(2):
+        minilm.encode_device(ids.data_ptr(), mask.data_ptr(), spec.batch, 128, out.data_ptr(), True,
+                             sa.cuda_stream)
+        minilm.encode_device(ids.data_ptr(), mask.data_ptr(), spec.batch, 0, out.data_ptr(), True,
+                             sb.cuda_stream)
+        minilm.synchronize()
+        assert (out.cpu().numpy() == 0).all()
+    minilm.encode_device(ids.data_ptr(), mask.data_ptr(), spec.batch, 128, out.data_ptr(), True,
+                         sb.cuda_stream)
+    minilm.synchronize()
+    norms = np.linalg.norm(out.cpu().numpy().astype(np.float64), axis=1)
+    np.testing.assert_allclose(norms, 1.0, atol=1e-5)
+
+
 def test_concurrent_callers_and_workspace_growth(env, minilm):
     """encode(&self) is shared by rayon workers (src/lib.rs:440-451): many host
     threads on one model give the results of serial calls, across workspace growth."""
@@ -686,6 +820,50 @@ def test_from_pretrained_path_safetensors(env, tmp_path, weights_for):
     np.testing.assert_array_equal(m1.encode_ids(ids, mask), m2.encode_ids(ids, mask))
     m1.close()
     m2.close()
+
+
+def _write_pretrained_dir(path, cfg, tensors):
+    from safetensors.torch import save_file
+    save_file(tensors, str(path / "model.safetensors"))
+    with open(path / "config.json", "w") as f:
+        json.dump({"hidden_size": cfg.hidden_size, "num_attention_heads": cfg.num_attention_heads,
+                   "num_hidden_layers": cfg.num_hidden_layers, "intermediate_size": cfg.intermediate_size,
+                   "vocab_size": cfg.vocab_size, "max_position_embeddings": cfg.max_position_embeddings,
+                   "layer_norm_eps": cfg.layer_norm_eps, "hidden_act": "gelu", "model_type": "bert"}, f)
+
+
+@pytest.mark.parametrize("file_dtype", ["F16", "BF16"])
+@pytest.mark.parametrize("model_dtype", ["fp32", "bf16"])
+def test_from_pretrained_path_half_precision(env, tmp_path, weights_for, orc, file_dtype, model_dtype):
+    """A model.safetensors holding F16 or BF16 tensors (MiniLM shape) is
+    uploaded in its own encoding and converted on the device.  Its vectors are
+    bit-identical to those of the same values handed over as f32 (widened in
+    torch), for fp32 and bf16 models; the fp32 model also matches the oracle
+    run on the widened weights."""
+    torch, eb, Nn, L = env
+    from edgebert_amd import synth
+    cfg = synth.MINILM_L6
+    w = weights_for(cfg)
+    tdt = torch.float16 if file_dtype == "F16" else torch.bfloat16
+    half = {k: torch.from_numpy(np.ascontiguousarray(v)).to(tdt) for k, v in w.items()}
+    widened = {k: v.float().numpy() for k, v in half.items()}
+    _write_pretrained_dir(tmp_path, cfg, half)
+    m_file = eb.Model.from_pretrained_path(str(tmp_path), dtype=model_dtype)
+    m_ref = eb.Model.from_weights(widened, cfg, model_dtype)
+    try:
+        spec = synth.CONFIGS["c2"]
+        ids, mask, _ = synth.make_inputs(spec)
+        got = m_file.encode_ids(ids, mask)
+        np.testing.assert_array_equal(got, m_ref.encode_ids(ids, mask))
+        if model_dtype == "fp32":
+            import oracle
+            sel = np.arange(0, spec.batch, 4)
+            want = oracle.OracleModel(cfg, widened).encode_unpadded(ids[sel], mask[sel], normalize=True)
+            assert np.abs(got[sel] - want).max() <= 1e-4
+            assert cosine_rows(got[sel], want).min() >= 0.99999
+    finally:
+        m_file.close()
+        m_ref.close()
 
 
 def test_bf16_minilm_c3(env, weights_for, orc):

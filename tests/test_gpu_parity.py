@@ -152,6 +152,28 @@ def test_bf16_bert_base(eb, oracle_mod, weights_for):
     assert err <= FP32_MAX_ABS and cos >= FP32_MIN_COS
 
 
+def test_c5_full_batch_bf16(eb, oracle_mod, weights_for):
+    """c5 at its configured size: BERT-base, 1024 x 128 tokens, bf16 GEMMs and
+    attention with fp32 accumulation.  Every row finite and unit-norm; a batch
+    permutation gives bit-identical rows; 16 sequences spread over the batch
+    against the fp32 oracle (cosine >= 0.999 each)."""
+    spec = eb.CONFIGS["c5"]
+    assert (spec.batch, spec.seq_len) == (1024, 128)
+    w = weights_for(spec.model)
+    ids, mask, _ = eb.make_inputs(spec)
+    m16 = gpu_model(eb, spec.model, w, "bf16")
+    got = m16.encode_ids(ids, mask, normalize=True)
+    assert got.shape == (1024, 768) and np.isfinite(got).all()
+    np.testing.assert_allclose(np.linalg.norm(got.astype(np.float64), axis=1), 1.0, atol=1e-5)
+    perm = np.random.default_rng(5).permutation(spec.batch)
+    got_p = m16.encode_ids(ids[perm], mask[perm], normalize=True)
+    assert np.array_equal(got_p, got[perm])
+    sel = np.arange(3, spec.batch, spec.batch // 16)[:16]
+    want = oracle_mod.OracleModel(spec.model, w).encode(ids[sel], mask[sel], normalize=True)
+    _, cos = _report("c5 full batch bf16, 16 sequences vs fp32 oracle", got[sel], want)
+    assert cos >= BF16_MIN_COS
+
+
 @pytest.mark.parametrize("model_name,B,S,lo,hi", [
     ("minilm", 1, 1, 1, 1), ("minilm", 5, 12, 3, 12), ("minilm", 4, 16, 16, 16),
     ("minilm", 8, 8, 2, 8), ("bert", 2, 24, 9, 24)])
