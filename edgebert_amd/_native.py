@@ -22,6 +22,7 @@ EBH_ERR_HIP = -5
 EBH_ERR_RANGE = -6
 EBH_DTYPE_F32 = 0
 EBH_DTYPE_BF16 = 1
+NOALLOC_SCRATCH_BYTES = 128 << 20   # EBH_NOALLOC_SCRATCH_BYTES
 EPI_BIAS, EPI_BIAS_GELU, EPI_BIAS_RESID, EPI_NONE = 0, 1, 2, 3
 PROF = {"none": 0, "gemm_qkv": 1, "attention": 2, "gemm_out": 3, "gemm_ffn_up": 4,
         "gemm_ffn_down": 5, "layernorm": 6, "embed": 7, "pool": 8}
@@ -56,6 +57,7 @@ _SIGS = {
     "ebh_forward": (_i32, [_vp, _vp, _vp, _i32, _i32, _vp]),
     "ebh_encode": (_i32, [_vp, _vp, _vp, _i32, _i32, _i32, _vp]),
     "ebh_encode_device": (_i32, [_vp, _vp, _vp, _i32, _i32, _i32, _vp, _vp]),
+    "ebh_encode_device_noalloc": (_i32, [_vp, _vp, _vp, _i32, _i32, _i32, _vp, _vp]),
     "ebh_score": (_i32, [_vp, _vp, _vp, _i32, _i32, _vp]),
     "ebh_score_device": (_i32, [_vp, _vp, _vp, _i32, _i32, _vp, _vp]),
     "ebh_synchronize": (_i32, [_vp]),

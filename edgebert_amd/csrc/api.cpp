@@ -151,6 +151,9 @@ struct ebh_model {
     std::vector<GraphEntry> graphs;
     uint64_t graph_clock = 0;
     bool graph_replay = true;
+    // ebh_encode_device_noalloc has run on this model: ebh_synchronize also
+    // reads the id-range flag of the device's static scratch workspace
+    bool noalloc_used = false;
     // profiling of one kernel family
     int prof_kind = EBH_PROF_NONE;
     std::vector<ProfPair> prof_events;
@@ -224,8 +227,8 @@ int check_config(const ebh_config& c) {
     return EBH_OK;
 }
 
-void prof_begin(ebh_model* m, int kind, hipStream_t s, ProfPair& pp, bool& on) {
-    on = (m->prof_kind == kind);
+void prof_begin(ebh_model* m, int active, int kind, hipStream_t s, ProfPair& pp, bool& on) {
+    on = (active == kind);
     if (!on) return;
     for (hipEvent_t* e : {&pp.a, &pp.b}) {
         if (!m->prof_free.empty()) {
@@ -250,28 +253,56 @@ void drop_graphs(ebh_model* m) {
     m->graphs.clear();
 }
 
+// Place a workspace for tcap tokens and bcap sequences at `base` (nullptr:
+// only count); returns the bytes it spans.  Few-token fp32 forwards split the
+// bias-free projections over K; Y then holds one partial product per split.
+size_t layout_workspace(const ebh_model* m, int64_t tcap, int bcap, char* base, Workspace& w) {
+    const ebh_config& c = m->cfg;
+    const size_t H = c.hidden_size, I = c.intermediate_size;
+    const bool b16 = m->dtype == EBH_DTYPE_BF16;
+    const int yparts = b16 ? 1
+                           : std::max(ebh::gemm_f32_splits((int)tcap, (int)H, (int)H),
+                                      ebh::gemm_f32_splits((int)tcap, (int)H, (int)I));
+    size_t off = 0;
+    auto take = [&](size_t bytes) { size_t o = off; off += align_up(std::max<size_t>(bytes, 1)); return o; };
+    const size_t oErr = take(4), oX = take(b16 ? 0 : tcap * H * 4), oX16 = take(b16 ? tcap * H * 2 : 0),
+                 oY = take((size_t)yparts * tcap * H * 4), oQKV = take(tcap * 3 * H * 4),
+                 oCTX = take(tcap * H * 4), oF = take(tcap * I * 4), oIds = take(tcap * 4),
+                 oMask = take(tcap * 4), oCounts = take(bcap * 4), oCu = take((bcap + 1) * 4),
+                 oNtok = take(4), oTid = take(tcap * 4), oTpos = take(tcap * 4),
+                 oOut = take((size_t)bcap * H * 4), oScores = take((size_t)bcap * 4);
+    if (!base) return off;
+    w.base = base;
+    w.tok_cap = tcap;
+    w.b_cap = bcap;
+    w.y_parts = yparts;
+    w.err = (int*)(base + oErr);
+    w.X = b16 ? nullptr : (float*)(base + oX);
+    w.X16 = b16 ? (uint16_t*)(base + oX16) : nullptr;
+    w.Y = (float*)(base + oY);
+    w.QKV = (float*)(base + oQKV);
+    w.CTX = (float*)(base + oCTX);
+    w.F = (float*)(base + oF);
+    w.ids = (int*)(base + oIds);
+    w.mask = (int*)(base + oMask);
+    w.counts = (int*)(base + oCounts);
+    w.cu = (int*)(base + oCu);
+    w.ntok = (int*)(base + oNtok);
+    w.tok_id = (int*)(base + oTid);
+    w.tok_pos = (int*)(base + oTpos);
+    w.out = (float*)(base + oOut);
+    w.scores = (float*)(base + oScores);
+    return off;
+}
+
 int ensure_workspace(ebh_model* m, int B, int S) {
     const int64_t T = (int64_t)B * S;
     Workspace& w = m->ws;
     if (w.base && T <= w.tok_cap && B <= w.b_cap) return EBH_OK;
     const int64_t tcap = std::max<int64_t>(T, w.tok_cap);
     const int bcap = std::max(B, w.b_cap);
-    const ebh_config& c = m->cfg;
-    const size_t H = c.hidden_size, I = c.intermediate_size;
-    // Few-token fp32 forwards split the bias-free projections over K; Y then
-    // holds one partial product per split.
-    const int yparts = m->dtype == EBH_DTYPE_BF16
-                           ? 1
-                           : std::max(ebh::gemm_f32_splits((int)tcap, (int)H, (int)H),
-                                      ebh::gemm_f32_splits((int)tcap, (int)H, (int)I));
-    size_t off = 0;
-    auto take = [&](size_t bytes) { size_t o = off; off += align_up(std::max<size_t>(bytes, 1)); return o; };
-    const size_t oX = take(tcap * H * 4), oX16 = take(m->dtype == EBH_DTYPE_BF16 ? tcap * H * 2 : 0),
-                 oY = take((size_t)yparts * tcap * H * 4), oQKV = take(tcap * 3 * H * 4),
-                 oCTX = take(tcap * H * 4), oF = take(tcap * I * 4), oIds = take(tcap * 4),
-                 oMask = take(tcap * 4), oCounts = take(bcap * 4), oCu = take((bcap + 1) * 4),
-                 oNtok = take(4), oTid = take(tcap * 4), oTpos = take(tcap * 4), oErr = take(4),
-                 oOut = take((size_t)bcap * H * 4), oScores = take((size_t)bcap * 4);
+    Workspace nw;
+    const size_t bytes = layout_workspace(m, tcap, bcap, nullptr, nw);
     // Work from the previous call may still use the old block, and recorded
     // forwards hold its addresses.  A raised id-range flag is carried over to
     // the new block (it stays raised until ebh_synchronize reads it).
@@ -280,32 +311,10 @@ int ensure_workspace(ebh_model* m, int B, int S) {
     int old_err = 0;
     if (w.base) HIP_TRY(hipMemcpy(&old_err, w.err, 4, hipMemcpyDeviceToHost));
     if (w.base) HIP_TRY(hipFree(w.base));
-    w.base = nullptr;
-    w.tok_cap = 0;
-    w.b_cap = 0;
+    w = Workspace{};
     void* base = nullptr;
-    HIP_TRY(hipMalloc(&base, off));
-    char* b = static_cast<char*>(base);
-    w.base = base;
-    w.tok_cap = tcap;
-    w.b_cap = bcap;
-    w.y_parts = yparts;
-    w.X = (float*)(b + oX);
-    w.X16 = m->dtype == EBH_DTYPE_BF16 ? (uint16_t*)(b + oX16) : nullptr;
-    w.Y = (float*)(b + oY);
-    w.QKV = (float*)(b + oQKV);
-    w.CTX = (float*)(b + oCTX);
-    w.F = (float*)(b + oF);
-    w.ids = (int*)(b + oIds);
-    w.mask = (int*)(b + oMask);
-    w.counts = (int*)(b + oCounts);
-    w.cu = (int*)(b + oCu);
-    w.ntok = (int*)(b + oNtok);
-    w.tok_id = (int*)(b + oTid);
-    w.tok_pos = (int*)(b + oTpos);
-    w.err = (int*)(b + oErr);
-    w.out = (float*)(b + oOut);
-    w.scores = (float*)(b + oScores);
+    HIP_TRY(hipMalloc(&base, bytes));
+    layout_workspace(m, tcap, bcap, static_cast<char*>(base), w);
     HIP_TRY(hipMemcpy(w.err, &old_err, 4, hipMemcpyHostToDevice));
     // The model's stream does not wait for the null stream: the flag must be
     // written before the first forward on this workspace can set it.
@@ -346,28 +355,31 @@ int ensure_host_staging(ebh_model* m, HostSlot& hs, int64_t T, int64_t outn) {
 // the un-normalised pooled rows left in d_out.
 // tokens: the number of mask == 1 tokens when the host knows it (the
 // blocking entry points), else -1.
-int enqueue_kernels(ebh_model* m, const int* d_ids, const int* d_mask, int B, int S,
-                    int normalize, float* d_out, hipStream_t s, float* d_scores, int64_t tokens) {
+// w: the workspace to run in (the model's own, or the no-allocation entry
+// point's static one); prof: time the profiled kernel family (creates events).
+int enqueue_kernels(ebh_model* m, Workspace& w, const int* d_ids, const int* d_mask, int B, int S,
+                    int normalize, float* d_out, hipStream_t s, float* d_scores, int64_t tokens,
+                    bool prof = true) {
     const ebh_config& c = m->cfg;
     const int H = c.hidden_size, I = c.intermediate_size, nh = c.num_attention_heads;
     const int hd = H / nh;
     const float eps = c.layer_norm_eps;
     const float scale = 1.0f / sqrtf((float)hd);  // src/lib.rs:196-197
-    Workspace& w = m->ws;
+    const int prof_kind = prof ? m->prof_kind : EBH_PROF_NONE;
     const int T = B * S;  // rows every kernel is sized for; they read the packed count on the device
 
     ProfPair pp{};
     bool on = false;
     const bool bf16 = m->dtype == EBH_DTYPE_BF16;
     if (ebh::pack_embed_few_fits(B, S, H)) {   // a few short sentences: one launch
-        prof_begin(m, EBH_PROF_EMBED, s, pp, on);
+        prof_begin(m, prof_kind, EBH_PROF_EMBED, s, pp, on);
         HIP_TRY(ebh::launch_pack_embed_few(d_ids, d_mask, B, S, w.cu, w.ntok, w.tok_id, w.tok_pos, w.err,
                                            m->word, m->pos, m->type0, m->emb_g, m->emb_b, c.vocab_size, H,
                                            eps, bf16 ? nullptr : w.X, w.X16, s));
         prof_end(m, s, pp, on);
     } else {
         HIP_TRY(ebh::launch_pack(d_ids, d_mask, B, S, w.counts, w.cu, w.ntok, w.tok_id, w.tok_pos, s));
-        prof_begin(m, EBH_PROF_EMBED, s, pp, on);
+        prof_begin(m, prof_kind, EBH_PROF_EMBED, s, pp, on);
         HIP_TRY(ebh::launch_embed_ln(w.tok_id, w.tok_pos, w.ntok, T, m->word, m->pos, m->type0,
                                      m->emb_g, m->emb_b, c.vocab_size, H, eps, bf16 ? nullptr : w.X, w.err,
                                      w.X16, s));
@@ -404,7 +416,7 @@ int enqueue_kernels(ebh_model* m, const int* d_ids, const int* d_mask, int B, in
         a.K = K;
         ProfPair p2{};
         bool on2 = false;
-        prof_begin(m, kind, s, p2, on2);
+        prof_begin(m, prof_kind, kind, s, p2, on2);
         hipError_t e = bf16 ? ebh::launch_gemm_bf16_act(a, epi, c16, s) : ebh::launch_gemm_f32(a, epi, s);
         prof_end(m, s, p2, on2);
         if (e != hipSuccess) return fail(EBH_ERR_HIP, "gemm launch failed: %s", hipGetErrorString(e));
@@ -465,7 +477,7 @@ int enqueue_kernels(ebh_model* m, const int* d_ids, const int* d_mask, int B, in
         a.ln_eps = eps;
         ProfPair p2{};
         bool on2 = false;
-        prof_begin(m, kind, s, p2, on2);
+        prof_begin(m, prof_kind, kind, s, p2, on2);
         hipError_t e = ebh::launch_gemm_f32_add_ln(a, s);
         prof_end(m, s, p2, on2);
         if (e != hipSuccess) return fail(EBH_ERR_HIP, "gemm launch failed: %s", hipGetErrorString(e));
@@ -476,7 +488,7 @@ int enqueue_kernels(ebh_model* m, const int* d_ids, const int* d_mask, int B, in
         if ((rc = gemm(EBH_PROF_GEMM_QKV, bf16 ? (const void*)w.X16 : w.X, H, L.wqkv, L.wqkv16, L.bqkv,
                        bf16 ? (void*)qkv16 : (void*)w.QKV, 3 * H, H, ebh::EPI_BIAS, bf16)))
             return rc;
-        prof_begin(m, EBH_PROF_ATTENTION, s, pp, on);
+        prof_begin(m, prof_kind, EBH_PROF_ATTENTION, s, pp, on);
         if (bf16)
             HIP_TRY(ebh::launch_attention_bf16(qkv16, w.cu, B, S, H, nh, hd, scale, ctx16, s));
         else
@@ -488,7 +500,7 @@ int enqueue_kernels(ebh_model* m, const int* d_ids, const int* d_mask, int B, in
             if ((rc = gemm(EBH_PROF_GEMM_OUT, bf16 ? (const void*)ctx16 : w.CTX, H, L.wo, L.wo16, nullptr,
                            w.Y, H, H, ebh::EPI_NONE, bf16, sp_out, T_od)))
                 return rc;
-            prof_begin(m, EBH_PROF_LAYERNORM, s, pp, on);
+            prof_begin(m, prof_kind, EBH_PROF_LAYERNORM, s, pp, on);
             HIP_TRY(add_ln(L.bo, L.ln1_g, L.ln1_b, sp_out));
             prof_end(m, s, pp, on);
         }
@@ -501,12 +513,12 @@ int enqueue_kernels(ebh_model* m, const int* d_ids, const int* d_mask, int B, in
             if ((rc = gemm(EBH_PROF_GEMM_FFN_DOWN, bf16 ? (const void*)f16 : w.F, I, L.w2, L.w216, nullptr,
                            w.Y, H, I, ebh::EPI_NONE, bf16, sp_down, T_od)))
                 return rc;
-            prof_begin(m, EBH_PROF_LAYERNORM, s, pp, on);
+            prof_begin(m, prof_kind, EBH_PROF_LAYERNORM, s, pp, on);
             HIP_TRY(add_ln(L.b2, L.ln2_g, L.ln2_b, sp_down));
             prof_end(m, s, pp, on);
         }
     }
-    prof_begin(m, EBH_PROF_POOL, s, pp, on);
+    prof_begin(m, prof_kind, EBH_PROF_POOL, s, pp, on);
     HIP_TRY(bf16 ? ebh::launch_pool_b16(w.X16, w.cu, B, H, S, normalize, d_out, s)
                  : ebh::launch_pool(w.X, w.cu, B, H, S, normalize, d_out, s));
     prof_end(m, s, pp, on);
@@ -583,7 +595,7 @@ int run_forward(ebh_model* m, const int* d_ids, const int* d_mask, int B, int S,
             HIP_TRY(hipMemcpyAsync(w.ids, hs->ids, T * 4, hipMemcpyHostToDevice, st));
             HIP_TRY(hipMemcpyAsync(w.mask, hs->mask, T * 4, hipMemcpyHostToDevice, st));
         }
-        int rc = enqueue_kernels(m, d_ids, d_mask, B, S, normalize, d_out, st, d_scores, tokens);
+        int rc = enqueue_kernels(m, w, d_ids, d_mask, B, S, normalize, d_out, st, d_scores, tokens);
         if (rc) return rc;
         if (host) {
             HIP_TRY(hipMemcpyAsync(hs->out, d_scores ? d_scores : d_out, n_out * 4, hipMemcpyDeviceToHost, st));
@@ -654,6 +666,44 @@ int check_dims(const ebh_model* m, int B, int S) {
     return EBH_OK;
 }
 
+}  // namespace
+
+// ---------------------------------------------------------------------------
+// Static scratch workspace of ebh_encode_device_noalloc: the activations of
+// one forward (laid out by layout_workspace, id-range flag first), held by
+// every device the library runs on until the process ends.  Host code never
+// uses the array's name as an address (on the host it is only a stand-in):
+// ebh_finalize looks its device address up once per device with
+// hipGetSymbolAddress, and every kernel argument, fill and copy uses that.
+// ---------------------------------------------------------------------------
+static __device__ __align__(256) unsigned char scratch[EBH_NOALLOC_SCRATCH_BYTES];
+
+namespace {
+constexpr int MAX_DEVICES = 64;
+std::mutex g_scratch_mu;
+char* g_scratch_ptr[MAX_DEVICES] = {};   // device address of `scratch` per device
+
+// Called by ebh_finalize with the model's device current: look the array up
+// on this device once and clear its id-range flag (the word every no-
+// allocation forward's flag occupies), ordered before any later work of the
+// model by the stream synchronisation that follows.
+int setup_scratch(int dev, hipStream_t s) {
+    if (dev < 0 || dev >= MAX_DEVICES) return fail(EBH_ERR_STATE, "device %d beyond %d devices", dev, MAX_DEVICES);
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    if (g_scratch_ptr[dev]) return EBH_OK;
+    void* p = nullptr;
+    HIP_TRY(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+    if (!p) return fail(EBH_ERR_HIP, "hipGetSymbolAddress returned no address for the scratch workspace");
+    HIP_TRY(ebh::launch_zero_words(p, 1, s));
+    HIP_TRY(hipStreamSynchronize(s));
+    g_scratch_ptr[dev] = static_cast<char*>(p);
+    return EBH_OK;
+}
+
+char* scratch_ptr(int dev) {
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    return dev >= 0 && dev < MAX_DEVICES ? g_scratch_ptr[dev] : nullptr;
+}
 }  // namespace
 
 namespace ebh {
@@ -757,6 +807,7 @@ int ebh_finalize(ebh_model* m, int32_t dtype) {
     const ebh_config& c = m->cfg;
     const size_t H = c.hidden_size, I = c.intermediate_size, L = c.num_hidden_layers;
     const bool b16 = dtype == EBH_DTYPE_BF16;
+    int rc0;
     // Layout of the single device weight block.  The four GEMM weights of a
     // layer are held once, in the form the forward reads: fp32 for fp32
     // models, bf16 for bf16 models; everything else is fp32.
@@ -781,6 +832,7 @@ int ebh_finalize(ebh_model* m, int32_t dtype) {
     HIP_TRY(hipGetDevice(&m->device));
     HIP_TRY(hipStreamCreateWithFlags(&m->stream, hipStreamNonBlocking));
     HIP_TRY(hipEventCreateWithFlags(&m->done, hipEventDisableTiming));
+    if ((rc0 = setup_scratch(m->device, m->stream))) return rc0;
     HIP_TRY(hipMalloc(&m->wbase, off));
     char* b = static_cast<char*>(m->wbase);
 
@@ -996,6 +1048,40 @@ int ebh_encode_device(ebh_model* m, const int32_t* ids, const int32_t* mask, int
     return run_forward(m, ids, mask, B, S, normalize ? 1 : 0, out, s, nullptr, nullptr);
 }
 
+int ebh_encode_device_noalloc(ebh_model* m, const int32_t* ids, const int32_t* mask, int32_t B, int32_t S,
+                              int32_t normalize, float* out, void* stream) {
+    int rc = check_model_ready(m);
+    if (rc) return rc;
+    if ((rc = check_dims(m, B, S))) return rc;
+    if (B == 0) return EBH_OK;
+    if (!ids || !mask || !out) return fail(EBH_ERR_INVALID_ARG, "null buffer");
+    Workspace w;
+    const int64_t T = (int64_t)B * S;
+    const size_t need = layout_workspace(m, T, B, nullptr, w);
+    if (need > (size_t)EBH_NOALLOC_SCRATCH_BYTES)
+        return fail(EBH_ERR_RANGE,
+                    "batch %d x %d needs %zu bytes of workspace, more than the %zu bytes of the static scratch "
+                    "of ebh_encode_device_noalloc (use ebh_encode_device)",
+                    B, S, need, (size_t)EBH_NOALLOC_SCRATCH_BYTES);
+    std::lock_guard<std::mutex> lk(m->mu);
+    HIP_TRY(hipSetDevice(m->device));
+    char* base = scratch_ptr(m->device);
+    if (!base) return fail(EBH_ERR_STATE, "no scratch workspace on device %d", m->device);
+    hipStream_t s = stream ? static_cast<hipStream_t>(stream) : m->stream;
+    if (m->has_done) HIP_TRY(hipStreamWaitEvent(s, m->done, 0));
+    if (S == 0) {
+        HIP_TRY(ebh::launch_zero_words(out, (int64_t)B * m->cfg.hidden_size, s));
+    } else {
+        layout_workspace(m, T, B, base, w);
+        if ((rc = enqueue_kernels(m, w, ids, mask, B, S, normalize ? 1 : 0, out, s, nullptr, -1, false)))
+            return rc;
+    }
+    HIP_TRY(hipEventRecord(m->done, s));
+    m->has_done = true;
+    m->noalloc_used = true;
+    return EBH_OK;
+}
+
 int ebh_score(ebh_model* m, const uint32_t* ids, const uint32_t* mask, int32_t B, int32_t S,
               float* scores) {
     int rc = check_model_ready(m);
@@ -1084,11 +1170,16 @@ int ebh_synchronize(ebh_model* m) {
     std::lock_guard<std::mutex> lk(m->mu);
     HIP_TRY(hipSetDevice(m->device));
     if (m->has_done) HIP_TRY(hipEventSynchronize(m->done));
-    if (!m->ws.base) return EBH_OK;
     int err = 0;
-    HIP_TRY(hipMemcpy(&err, m->ws.err, 4, hipMemcpyDeviceToHost));
+    for (int* flag : {m->ws.base ? m->ws.err : nullptr,
+                      m->noalloc_used ? reinterpret_cast<int*>(scratch_ptr(m->device)) : nullptr}) {
+        if (!flag) continue;
+        int e = 0;
+        HIP_TRY(hipMemcpy(&e, flag, 4, hipMemcpyDeviceToHost));
+        if (e) HIP_TRY(hipMemset(flag, 0, 4));
+        err |= e;
+    }
     if (err) {
-        HIP_TRY(hipMemset(m->ws.err, 0, 4));
         HIP_TRY(hipStreamSynchronize(nullptr));  // cleared before the next forward can set it
         return fail(EBH_ERR_RANGE, "token id out of range for vocab %d", m->cfg.vocab_size);
     }

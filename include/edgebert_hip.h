@@ -130,6 +130,25 @@ EBH_API int ebh_encode(ebh_model* m, const uint32_t* ids, const uint32_t* mask, 
 EBH_API int ebh_encode_device(ebh_model* m, const int32_t* ids, const int32_t* mask, int32_t B,
                       int32_t S, int32_t normalize, float* out, void* stream);
 
+/* No counterpart in the reference: ebh_encode_device for callers that cannot
+ * allocate device memory (tight serving loops, harnesses that forbid
+ * hipMalloc, code that must not allocate once running).  Same arguments,
+ * results and ordering as
+ * ebh_encode_device, but the forward's workspace is a static device array of
+ * EBH_NOALLOC_SCRATCH_BYTES per device (held from the library's load until the
+ * process ends), so the call makes no hipMalloc / hipFree and records no
+ * graph.  A batch whose workspace does not fit fails with EBH_ERR_RANGE
+ * before anything is enqueued (128 MiB: MiniLM-L6 about 7k tokens in fp32,
+ * 9k in bf16, e.g. 56 x 128; BERT-base about 3.5k in fp32, 4.4k in bf16).
+ * Every call on one device shares that array: calls that overlap on a device
+ * (other models, other streams, other threads) race; calls on one model are
+ * ordered as ebh_encode_device's are.  Its id-range flag is the first word of
+ * the array, reported and cleared by ebh_synchronize of a model that ran this
+ * entry point.  ebh_last_tokens does not cover these forwards. */
+#define EBH_NOALLOC_SCRATCH_BYTES (128u << 20)
+EBH_API int ebh_encode_device_noalloc(ebh_model* m, const int32_t* ids, const int32_t* mask, int32_t B,
+                                      int32_t S, int32_t normalize, float* out, void* stream);
+
 /* Cross-encoder scoring (Model::score_pair / score_batch, src/lib.rs:327-383):
  * each row of ids / mask [B, S] (u32, zero-padded, as ebh_encode) is one
  * tokenised "query [SEP] document" pair; scores[b] = mean_pool(forward)[b] .
