@@ -9,7 +9,9 @@ import os
 import re
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(_HERE, "libedgebert_hip.so")
+# EDGEBERT_HIP_LIB selects another build of the same sources (the host
+# sanitizer build of `make -C edgebert_amd/csrc sanitize`).
+LIB_PATH = os.environ.get("EDGEBERT_HIP_LIB") or os.path.join(_HERE, "libedgebert_hip.so")
 HEADERS = [os.path.join(os.path.dirname(_HERE), "include", h)
            for h in ("edgebert_hip.h", "edgebert_hip_ops.h")]
 
@@ -124,7 +126,8 @@ def lib():
 
 
 def last_error() -> str:
-    return lib().ebh_last_error().decode()
+    # messages quote names taken from the caller's files, which may hold any bytes
+    return lib().ebh_last_error().decode("utf-8", errors="replace")
 
 
 def check(rc: int):

@@ -23,7 +23,9 @@ _i64p = ctypes.POINTER(ctypes.c_int64)
 def lib():
     global _LIB
     if _LIB is None:
-        path = os.path.join(_HERE, "liboracle.so")
+        # EDGEBERT_ORACLE_LIB selects another build (the sanitizer build of
+        # `make -C oracle sanitize`).
+        path = os.environ.get("EDGEBERT_ORACLE_LIB") or os.path.join(_HERE, "liboracle.so")
         if not os.path.exists(path):
             raise RuntimeError(f"{path} is missing: build it with `make -C oracle` "
                                "(or __graft_entry__.build())")
