@@ -346,9 +346,14 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_persistent_kernel
         l_r[i] = P / CPR;
         l_c[i] = EPC * ((P % CPR) ^ chunk_swizzle16<CPR>(P / CPR));   // elements
     }
-    // Source pointers of the next k-tile to load (iteration `nit`), advanced by BK
-    // per k-tile and recomputed when that k-tile starts a new C tile.
-    const char* src[NL];                          // byte addresses
+    // Sources of the next k-tile to load (iteration `nit`): the A and W panel
+    // bases of that k-tile (wave-uniform, in SGPRs, advanced by BK per k-tile)
+    // and this lane's byte offsets from them (32-bit, fixed for a C tile: the
+    // row, clamped to the last real row, and the swizzled k-chunk).  Offsets
+    // instead of per-load 64-bit addresses keep the k-loop's addressing off
+    // the VGPRs.
+    uint32_t soff[NL];
+    uint64_t abase = 0, wbase = 0;
     const float* bias_src = nullptr;
     int nit = 0;
     auto point_at = [&](int it) {
@@ -357,8 +362,10 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_persistent_kernel
         const int mt = t / ntiles_n, m0 = mt * BM, n0 = (t - mt * ntiles_n) * BN;
 #pragma unroll
         for (int i = 0; i < NL; ++i)
-            src[i] = i < LA ? A + ((int64_t)min(m0 + l_r[i], M - 1) * p.lda + kt * BK + l_c[i]) * ES
-                            : W + ((int64_t)min(n0 + l_r[i], N - 1) * p.ldw + kt * BK + l_c[i]) * ES;
+            soff[i] = i < LA ? (uint32_t)(((min(m0 + l_r[i], M - 1) - m0) * p.lda + l_c[i]) * ES)
+                             : (uint32_t)(((min(n0 + l_r[i], N - 1) - n0) * p.ldw + l_c[i]) * ES);
+        abase = uniform_u64(A + ((int64_t)m0 * p.lda + kt * BK) * ES);
+        wbase = uniform_u64(W + ((int64_t)n0 * p.ldw + kt * BK) * ES);
         if (HAS_BIAS) bias_src = p.bias + min(n0 + wn * WN + 4 * lane, N - 4);
     };
     // Load instructions of k-tile j (the bias chunk rides with a tile's first k-tile).
@@ -377,7 +384,8 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_persistent_kernel
 #pragma unroll
         for (int i = 0; i < NL; ++i)
             if (i / PER == part)
-                load_lds16_async(src[i], st + (i < LA ? 0 : BM * RW) + ((i < LA ? i : i - LA) * NT + wave * 64) * 4);
+                load_lds16_sbase(i < LA ? abase : wbase, soff[i],
+                                 st + (i < LA ? 0 : BM * RW) + ((i < LA ? i : i - LA) * NT + wave * 64) * 4);
         if (part == NPART - 1) {
             if (HAS_BIAS && nit % nk == 0)
                 load_lds16_async(bias_src, smem + NSTAGE * STAGE + (((nit / nk) & 1) * NW + wave) * BIAS_SLOT);
@@ -386,8 +394,8 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_persistent_kernel
                 if (nit % nk == 0) {
                     point_at(nit);
                 } else {
-#pragma unroll
-                    for (int i = 0; i < NL; ++i) src[i] += BK * ES;
+                    abase += BK * ES;
+                    wbase += BK * ES;
                 }
             }
         }
@@ -572,6 +580,9 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_persistent_kernel
         const float* bslot = smem + NSTAGE * STAGE + ((t & 1) * NW + wave) * BIAS_SLOT;
         float* cw = const_cast<float*>(cs_base) + wave * (16 * WN);
         constexpr int NPASS = 4 * WN / 64;
+        // lane-derived offsets opaque here (computed at the stores, not held)
+        int fl = lane, fl32 = l32, fhalf = half;
+        asm volatile("" : "+v"(fl), "+v"(fl32), "+v"(fhalf));
 #pragma unroll
         for (int i = 0; i < FM; ++i)
 #pragma unroll
@@ -580,10 +591,10 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_persistent_kernel
                 for (int j = 0; j < FN; ++j)
 #pragma unroll
                     for (int rr = 0; rr < 8; ++rr)
-                        cw[(8 * (rr >> 2) + 4 * half + (rr & 3)) * WN + j * 32 + l32] = acc[i][j][8 * h + rr];
+                        cw[(8 * (rr >> 2) + 4 * fhalf + (rr & 3)) * WN + j * 32 + fl32] = acc[i][j][8 * h + rr];
 #pragma unroll
                 for (int ps = 0; ps < NPASS; ++ps) {
-                    const int q = ps * 64 + lane, lr = q / C4, c = 4 * (q - lr * C4);
+                    const int q = ps * 64 + fl, lr = q / C4, c = 4 * (q - lr * C4);
                     const float4 v = *reinterpret_cast<const float4*>(cw + lr * WN + c);
                     float4 b4 = make_float4(0, 0, 0, 0);
                     if (HAS_BIAS) b4 = *reinterpret_cast<const float4*>(bslot + c);
@@ -595,13 +606,17 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_persistent_kernel
         const int u = wg + t * G, split = u / ntiles, tile = u - split * ntiles;
         float* const Cs = p.C + (int64_t)split * p.split_stride;
         const int m0 = (tile / ntiles_n) * BM, n0 = (tile - (tile / ntiles_n) * ntiles_n) * BN;
-        const int gc = n0 + wn * WN + e_c;
+        // The lane's place in the tile, opaque here: the row addresses derived
+        // from it are computed at the stores, not held across the k-loop.
+        int er = e_r, ec = e_c;
+        asm volatile("" : "+v"(er), "+v"(ec));
+        const int gc = n0 + wn * WN + ec;
         const bool col_ok = gc < N;  // N % 4 == 0: all 4 columns or none
         float4 bias4 = make_float4(0, 0, 0, 0);
         if (HAS_BIAS)
-            bias4 = *reinterpret_cast<const float4*>(smem + NSTAGE * STAGE + ((t & 1) * NW + wave) * BIAS_SLOT + e_c);
+            bias4 = *reinterpret_cast<const float4*>(smem + NSTAGE * STAGE + ((t & 1) * NW + wave) * BIAS_SLOT + ec);
         float* cw = const_cast<float*>(cs_base) + wave * (32 * WN);
-        const int grow0 = m0 + wm * WM + e_r;
+        const int grow0 = m0 + wm * WM + er;
 #pragma unroll
         for (int i = 0; i < FM; ++i) {
 #pragma unroll
@@ -611,7 +626,7 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_persistent_kernel
                     cw[(8 * (r >> 2) + 4 * half + (r & 3)) * WN + j * 32 + l32] = acc[i][j][r];
 #pragma unroll
             for (int qq = 0; qq < NPB; ++qq) {
-                float4 v = *reinterpret_cast<const float4*>(cw + (qq * RPP + e_r) * WN + e_c);
+                float4 v = *reinterpret_cast<const float4*>(cw + (qq * RPP + er) * WN + ec);
                 if (HAS_BIAS) { v.x += bias4.x; v.y += bias4.y; v.z += bias4.z; v.w += bias4.w; }
                 if constexpr (EPI == EPI_BIAS_GELU) {
                     v.x = gelu_tanh_fast(v.x); v.y = gelu_tanh_fast(v.y);

@@ -196,6 +196,33 @@ __device__ __forceinline__ void load_lds16_async(const void* g, const float* lds
         : "memory");
 }
 
+// A pointer every lane of the wave holds, as a wave-uniform 64-bit value
+// (readfirstlane of each half; the casts keep the low half from being
+// sign-extended into the high one).
+__device__ __forceinline__ uint64_t uniform_u64(const void* p) {
+    const uint64_t b = (uint64_t)(uintptr_t)p;
+    return ((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(b >> 32)) << 32) |
+           (uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)b);
+}
+
+// load_lds16_async with the global address split as a wave-uniform 64-bit
+// base (SGPR pair) plus this lane's 32-bit byte offset: the saddr form of
+// global_load_lds_dwordx4.
+__device__ __forceinline__ void load_lds16_sbase(uint64_t sbase, uint32_t voff, const float* lds) {
+    const uint32_t base = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)lds);
+    const void* sb = (const void*)(uintptr_t)sbase;
+    uint32_t saved;
+    asm volatile(
+        "s_mov_b32 %0, m0\n\t"
+        "s_mov_b32 m0, %3\n\t"
+        "s_nop 0\n\t"
+        "global_load_lds_dwordx4 %1, %2\n\t"
+        "s_mov_b32 m0, %0"
+        : "=&s"(saved)
+        : "v"(voff), "s"(sb), "s"(base)
+        : "memory");
+}
+
 // At most n vector-memory operations of this wave outstanding (n is
 // wave-uniform; s_waitcnt takes an immediate, so switch over the counter's
 // range, 0..63; larger n waits for everything, which is always safe).
