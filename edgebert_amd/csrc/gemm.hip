@@ -689,7 +689,12 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_persistent_kernel
                 if (grow < M && gcol < N) {   // N % 4 == 0: the chunk's first 4 columns are in
                     uint16_t* dst = Cs + (int64_t)grow * p.ldc + gcol;
                     if (wide && gcol + 8 <= N) {
-                        *reinterpret_cast<uint4*>(dst) = d;
+                        // Streaming store: the output is consumed by a later
+                        // kernel, not this one (bf16 products at c5: QKV 511 ->
+                        // 499 us, FFN up 766 -> 749 us; the same hint on the fp32
+                        // epilogues measured 1-2% slower and is not used there).
+                        typedef unsigned int u4v __attribute__((ext_vector_type(4)));
+                        __builtin_nontemporal_store(u4v{d.x, d.y, d.z, d.w}, reinterpret_cast<u4v*>(dst));
                     } else {
                         *reinterpret_cast<uint2*>(dst) = make_uint2(d.x, d.y);
                         if (gcol + 8 <= N) *reinterpret_cast<uint2*>(dst + 4) = make_uint2(d.z, d.w);
