@@ -277,7 +277,7 @@ constexpr int BUFFER_RSRC_WORD3 = 0x00020000;
 // accumulators (epilogue_packed).  LDS offsets below are in
 // 4-byte words, so both element types share the layout and the swizzle.
 template <bool BF16, bool OUT16, int BM, int BN, int BK, int WAVES_M, int WAVES_N, int NSTAGE, int EPI,
-          bool SPREAD = BF16>
+          bool SPREAD = BF16, bool PREFETCH = BF16>
 __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_persistent_kernel(GemmArgs p) {
     constexpr int ES = BF16 ? 2 : 4;              // bytes per element
     constexpr int EPC = 16 / ES;                  // elements per 16-byte chunk
@@ -371,13 +371,15 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_persistent_kernel
     // Load instructions of k-tile j (the bias chunk rides with a tile's first k-tile).
     auto n_issued = [&](int j) { return NL + (HAS_BIAS && j % nk == 0 ? 1 : 0); };
     // The loads of a k-tile go out in parts: all at once, or (SPREAD) one part
-    // before each k-slice's MFMAs.  The CU's vector memory path takes about
-    // one 1 KB load per 20 cycles and a wave stalls at issue while it is backed
-    // up; at bf16 rates a k-tile's loads need over half of its MFMA time on
-    // that path, so issuing them as one burst after the barrier would idle the
-    // MFMA pipes.  Part `part` of NPART issues loads [part * PER, (part + 1) *
-    // PER); the last part adds the bias chunk and moves on to the next k-tile.
-    constexpr int NPART = SPREAD ? KS : 1;
+    // before each of the first half of the k-slices' MFMAs.  The CU's vector
+    // memory path takes one 1 KB load per 16 cycles, and a wave stalls at
+    // issue while it is backed up; at bf16 rates a k-tile's loads need half of
+    // its MFMA time on that path, so one burst after the barrier would idle
+    // the MFMA pipes, while parts spread over all k-slices leave the last
+    // loads too little time to land before the next k-tile's wait.  Part
+    // `part` of NPART issues loads [part * PER, (part + 1) * PER); the last
+    // part adds the bias chunk and moves on to the next k-tile.
+    constexpr int NPART = SPREAD && KS > 1 ? KS / 2 : 1;
     constexpr int PER = (NL + NPART - 1) / NPART;
     auto issue_part = [&](int part) {
         float* st = smem + (nit % NSTAGE) * STAGE;
@@ -738,17 +740,28 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_persistent_kernel
             const bool refill = nit < total;
             if (!SPREAD && refill) issue();
             const float* st = smem + (it % NSTAGE) * STAGE;
-#pragma unroll
-            for (int s = 0; s < KS; ++s) {
-                if (SPREAD && refill) issue_part(s);
+            // PREFETCH: k-slice s + 1's fragments are read while slice s's
+            // MFMAs run (two fragment sets in registers); otherwise each
+            // slice reads its own just before its MFMAs.
+            constexpr bool PREF = PREFETCH && KS > 1;
+            v4f afb[PREF ? 2 : 1][FM], wfb[PREF ? 2 : 1][FN];
+            auto rd = [&](int s, int b) __attribute__((always_inline)) {
                 const int ko = 4 * ((2 * s + half) ^ sw);
-                v4f af[FM], wf[FN];
 #pragma unroll
                 for (int i = 0; i < FM; ++i)
-                    af[i] = *reinterpret_cast<const v4f*>(st + a_row + i * 32 * RW + ko);
+                    afb[b][i] = *reinterpret_cast<const v4f*>(st + a_row + i * 32 * RW + ko);
 #pragma unroll
                 for (int j = 0; j < FN; ++j)
-                    wf[j] = *reinterpret_cast<const v4f*>(st + w_row + j * 32 * RW + ko);
+                    wfb[b][j] = *reinterpret_cast<const v4f*>(st + w_row + j * 32 * RW + ko);
+            };
+            if (PREF) rd(0, 0);
+#pragma unroll
+            for (int s = 0; s < KS; ++s) {
+                if (SPREAD && refill && s < NPART) issue_part(s);
+                if (!PREF) rd(s, 0);
+                else if (s + 1 < KS) rd(s + 1, (s + 1) & 1);
+                const v4f (&af)[FM] = afb[PREF ? (s & 1) : 0];
+                const v4f (&wf)[FN] = wfb[PREF ? (s & 1) : 0];
                 if constexpr (BF16) {
 #pragma unroll
                     for (int i = 0; i < FM; ++i)
