@@ -23,6 +23,8 @@
 // 8*(r/4) + 4*(l/32) + r%4 of its own query l%32, so the online-softmax
 // rescale and the final division use the lane's own statistics, and the
 // context leaves as 16-byte stores of four consecutive dims.
+#include <algorithm>
+
 #include "kernels.hpp"
 
 namespace ebh {
@@ -386,10 +388,198 @@ __global__ __launch_bounds__(256) void attention_bf16_kernel(const uint16_t* __r
     }
 }
 
+// ---------------------------------------------------------------------------
+// bf16 attention for sequences of at most 128 tokens: one key chunk and one
+// query block per (head, sequence) workgroup.  K and V go straight from HBM
+// into LDS (global_load_lds_dwordx4, no staging registers, no transposing
+// copy), so a workgroup needs 32 KB of LDS and about 150 VGPRs: three
+// workgroups per CU, whose load phases overlap each other's MFMAs and
+// softmax.
+//
+// K rows sit unpadded with 16-byte chunk c of row r at c ^ chunk_swizzle16(r)
+// (conflict-free fragment reads down 32 rows), as the GEMM tiles do.  V stays
+// row-major ([key][dim]): the A operand of O^T = V^T . P^T needs, per lane,
+// one dim at 8 keys, which ds_read_b64_tr_b16 delivers.  Within each 16-lane
+// group that instruction hands lane i element i % 4 of the 8-byte reads of
+// lanes i / 4, 4 + i / 4, 8 + i / 4 and 12 + i / 4; so when lane j of the
+// group addresses key k0 + j / 4, dims d0 + 4 (j % 4) .. +3, lane i receives
+// dim d0 + i at the four keys k0 .. k0 + 3.  Two such reads give a lane its 8
+// keys of one MFMA.  V chunk c of row r sits at c ^ 4 ((r >> 1) & 1) (64-dim
+// rows), so the four rows a half-wave reads fall in different banks.
+// ---------------------------------------------------------------------------
+typedef short v4s_t __attribute__((ext_vector_type(4)));
+
+template <int HD>
+__device__ __forceinline__ int v_swizzle(int r) {
+    return HD == 64 ? 4 * ((r >> 1) & 1) : 0;
+}
+
+template <int HD>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) void attention_bf16_short_kernel(
+    const uint16_t* __restrict__ qkv, const int* __restrict__ cu_seqlens, uint16_t* __restrict__ ctx, int H,
+    float scale) {
+    constexpr int KC = 128;                 // keys (and queries) per sequence at most
+    constexpr int CPR = HD / 8;             // 16-byte chunks per K / V row
+    constexpr int TILE = KC * HD;           // bf16 elements of the K or V tile
+    constexpr int NLD = KC * CPR / 256;     // 16-byte loads per thread per tile
+    constexpr int NJ = HD / 32;             // 32-wide blocks of the context
+    constexpr int NS = HD / 16;             // 16-dim slices of q.k
+    __shared__ __attribute__((aligned(16))) uint16_t Ks[TILE];
+    __shared__ __attribute__((aligned(16))) uint16_t Vs[TILE];
+
+    const int head = blockIdx.x, b = blockIdx.y;
+    const int start = cu_seqlens[b];
+    const int len = cu_seqlens[b + 1] - start;
+    if (len == 0) return;  // uniform over the workgroup
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int l32 = lane & 31, half = lane >> 5;
+    const int64_t ld = 3 * (int64_t)H;
+    const uint16_t* Qg = qkv + (int64_t)start * ld + head * HD;
+    const uint16_t* Kg = Qg + H;
+    const uint16_t* Vg = Qg + 2 * H;
+
+    // K and V into LDS: wave w's load i fills 16-byte slots (4 i + w) * 64 +
+    // lane, i.e. row P / CPR, stored chunk P % CPR.  Rows past the sequence
+    // re-read its last row (their keys are masked, their V rows meet zero
+    // probabilities).
+#pragma unroll
+    for (int i = 0; i < NLD; ++i) {
+        const int P = (i * 4 + wave) * 64 + lane;
+        const int r = P / CPR, pc = P % CPR;
+        const int64_t row = (int64_t)min(r, len - 1) * ld;
+        load_lds16_async(Kg + row + 8 * (pc ^ chunk_swizzle16<CPR>(r)),
+                         reinterpret_cast<const float*>(Ks + (i * 4 + wave) * 512));
+        load_lds16_async(Vg + row + 8 * (pc ^ v_swizzle<HD>(r)),
+                         reinterpret_cast<const float*>(Vs + (i * 4 + wave) * 512));
+    }
+    // This lane's query as the B operand: dims 16s + 8*half .. +7.
+    const int qi = min(wave * 32 + l32, len - 1);
+    v8s_t qf[NS];
+#pragma unroll
+    for (int s = 0; s < NS; ++s)
+        qf[s] = *reinterpret_cast<const v8s_t*>(Qg + (int64_t)qi * ld + 16 * s + 8 * half);
+    wait_vmcnt(0);
+    __syncthreads();
+
+    const int nkb = (len + 31) / 32;     // 32-key blocks holding real keys
+    // S^T = K . Q^T: the four 32-key blocks' MFMA chains side by side.
+    v16f sc[4];
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) sc[kb][r] = 0.0f;
+#pragma unroll
+    for (int s = 0; s < NS; ++s)
+#pragma unroll
+        for (int kb = 0; kb < 4; ++kb)
+            if (kb < nkb) {
+                const int kr = kb * 32 + l32;
+                const v8s_t kf = *reinterpret_cast<const v8s_t*>(
+                    Ks + kr * HD + 8 * ((2 * s + half) ^ chunk_swizzle16<CPR>(kr)));
+                sc[kb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(v8bf_t, kf),
+                                                                  __builtin_bit_cast(v8bf_t, qf[s]), sc[kb], 0, 0, 0);
+            }
+    // Row max of the raw scores (scale > 0 commutes with max); keys past the
+    // sequence (only in its last block) are masked to -inf (src/lib.rs:887-891).
+    float cmax = -INFINITY;
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb) {
+        if (kb < nkb) {
+            if ((kb + 1) * 32 > len) {
+#pragma unroll
+                for (int r = 0; r < 16; ++r)
+                    if (kb * 32 + 8 * (r >> 2) + 4 * half + (r & 3) >= len) sc[kb][r] = -INFINITY;
+            }
+#pragma unroll
+            for (int r = 0; r < 16; ++r) cmax = fmaxf(cmax, sc[kb][r]);
+        }
+    }
+    cmax = fmaxf(cmax, __shfl_xor(cmax, 32));
+    // p = exp(scale * (s - max)) as exp2(s * c - max * c), c = scale * log2(e):
+    // the scale after q.k^T (src/lib.rs:714) folded into one FMA.
+    const float c2 = scale * 1.4426950408889634f, off = -cmax * c2;
+    float psum = 0.0f;
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb) {
+        if (kb < nkb) {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const float pr = __builtin_amdgcn_exp2f(fmaf(sc[kb][r], c2, off));
+                sc[kb][r] = pr;
+                psum += pr;
+            }
+        }
+    }
+    v16f o[NJ];
+#pragma unroll
+    for (int j = 0; j < NJ; ++j)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) o[j][r] = 0.0f;
+    // context^T += V^T . P^T, two 16-key MFMAs per 32-key block.  Lane half h
+    // of the B operand (P) holds keys 16 mm + 4 h + 0..3 and 16 mm + 8 + 4 h +
+    // 0..3; the A operand (V^T) gets the same keys at dim l32 from two
+    // transposing reads.  16-lane group g reads dims 16 (g % 2) .. +15 of its
+    // 32-dim block at keys k0 .. k0 + 3.
+    const int g16 = lane >> 4, i16 = lane & 15;
+    const int vrow = i16 >> 2, vdim = 16 * (g16 & 1) + 4 * (i16 & 3);
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb) {
+        if (kb < nkb) {
+#pragma unroll
+            for (int mm = 0; mm < 2; ++mm) {
+                const float* pf = reinterpret_cast<const float*>(&sc[kb]) + 8 * mm;
+                const v8s_t pa = __builtin_bit_cast(
+                    v8s_t, make_uint4(pack_bf16x2(pf[0], pf[1]), pack_bf16x2(pf[2], pf[3]),
+                                      pack_bf16x2(pf[4], pf[5]), pack_bf16x2(pf[6], pf[7])));
+                const int k0 = kb * 32 + 16 * mm + 4 * (g16 >> 1);   // this group's first key
+#pragma unroll
+                for (int j = 0; j < NJ; ++j) {
+                    const int d = j * 32 + vdim;                     // this lane's 4 dims to address
+                    const int ra = k0 + vrow, rb = k0 + 8 + vrow;
+                    const v4s_t va = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                        (__attribute__((address_space(3))) v4s_t*)(Vs + ra * HD + 8 * ((d >> 3) ^ v_swizzle<HD>(ra)) + (d & 7)));
+                    const v4s_t vb = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                        (__attribute__((address_space(3))) v4s_t*)(Vs + rb * HD + 8 * ((d >> 3) ^ v_swizzle<HD>(rb)) + (d & 7)));
+                    const v8s_t vf = {va[0], va[1], va[2], va[3], vb[0], vb[1], vb[2], vb[3]};
+                    o[j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(v8bf_t, vf),
+                                                                    __builtin_bit_cast(v8bf_t, pa), o[j], 0, 0, 0);
+                }
+            }
+        }
+    }
+    // Lane holds dims j*32 + 8*g + 4*half + 0..3 (g = r / 4) of query l32.
+    const float l_tot = psum + __shfl_xor(psum, 32);
+    const int q = wave * 32 + l32;
+    if (q < len) {
+        const float inv = 1.0f / l_tot;
+        uint16_t* dst = ctx + (int64_t)(start + q) * H + head * HD + 4 * half;
+#pragma unroll
+        for (int j = 0; j < NJ; ++j)
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                *reinterpret_cast<uint2*>(dst + j * 32 + 8 * g) =
+                    make_uint2(pack_bf16x2(o[j][4 * g] * inv, o[j][4 * g + 1] * inv),
+                               pack_bf16x2(o[j][4 * g + 2] * inv, o[j][4 * g + 3] * inv));
+            }
+    }
+}
+
 hipError_t launch_attention_bf16(const uint16_t* qkv, const int* cu_seqlens, int B, int max_len,
                                  int H, int nh, int head_dim, float scale, uint16_t* ctx,
                                  hipStream_t s) {
     if (B <= 0 || max_len <= 0) return hipSuccess;
+    if (max_len <= 128) {
+        // One key chunk per sequence: K and V straight into LDS, three
+        // workgroups per CU.
+        const dim3 grid(nh, B), block(256);
+        if (head_dim == 32)
+            hipLaunchKernelGGL(attention_bf16_short_kernel<32>, grid, block, 0, s, qkv, cu_seqlens, ctx, H, scale);
+        else if (head_dim == 64)
+            hipLaunchKernelGGL(attention_bf16_short_kernel<64>, grid, block, 0, s, qkv, cu_seqlens, ctx, H, scale);
+        else
+            return hipErrorInvalidValue;
+        return hipGetLastError();
+    }
     const dim3 grid(nh, (max_len + 127) / 128, B), block(256);
     if (head_dim == 32)
         hipLaunchKernelGGL(attention_bf16_kernel<32>, grid, block, 0, s, qkv, cu_seqlens, ctx, H, scale);

@@ -323,15 +323,26 @@ def test_attention(env, H, nh, lengths):
     np.testing.assert_allclose(dctx.cpu().numpy(), attention64(qkv, cu, H, nh), rtol=0, atol=2e-5)
 
 
+_SHORT_RAGGED = [int(x) for x in np.random.default_rng(7).integers(1, 129, 120)]
+
+
 @pytest.mark.parametrize("H,nh,lengths", [
     (384, 12, [1, 2, 31, 32, 33, 127, 128, 129]),
     (384, 12, [256, 300, 511, 512]),
     (768, 12, [1, 64, 128, 130, 257]),
     (64, 2, [5, 17]),
+    (768, 12, [128, 1, 64, 100, 0, 77, 128, 33]),
+    (384, 12, [1, 2, 31, 32, 33, 127, 128, 0]),
+    (384, 12, _SHORT_RAGGED),
+    (768, 12, _SHORT_RAGGED[:60]),
 ])
 def test_attention_bf16(env, H, nh, lengths):
     """bf16 q / k / v and context: the float64 attention of the same bf16 values,
-    within the bf16 rounding of the probabilities and of the result."""
+    within the bf16 rounding of the probabilities and of the result.  Batches
+    whose sequences all have at most 128 tokens take the persistent kernel
+    (sequence x head items walked by each workgroup, the next item's K / V
+    prefetched): with empty sequences, and with 1,440 and 720 items, more
+    than the grid's workgroups."""
     torch, eb, Nn, L = env
     rng = np.random.default_rng(sum(lengths) + H + 1)
     T = sum(lengths)
