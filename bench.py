@@ -40,7 +40,9 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 # MI355X published dense peaks: fp32 matrix 157.3 TFLOP/s, bf16 2.5 PFLOP/s; HBM3E 8 TB/s.
-PEAK_TFLOPS = {"fp32": 157.3, "bf16": 2500.0}
+# Dense matrix peaks of MI355X per algorithmic flop: fp32 MFMA, bf16 MFMA, and
+# fp32 products formed from six bf16 MFMA products (the bf16 peak / 6).
+PEAK_TFLOPS = {"fp32": 157.3, "bf16": 2500.0, "fp32-bf16x6": 2500.0 / 6}
 HBM_PEAK_GBS = 8000.0
 KERNELS = ("gemm_qkv", "attention", "gemm_out", "gemm_ffn_up", "gemm_ffn_down", "layernorm",
            "embed", "pool")
@@ -190,13 +192,74 @@ def text_path(model, spec, ids, mask, lengths, steps: int) -> dict:
     return out
 
 
+def split_product_run(eb, torch, spec, weights, d_ids, d_mask, d_ref, lengths, steps, warmup,
+                      profile_kernel, graph_replay):
+    """The same workload on an EBH_DTYPE_F32_BF16X6 model: fp32 weights and
+    activations, every large GEMM product formed from six bf16 MFMA products
+    of three-way bf16 splits (fp32 accumulate).  Reported beside the headline,
+    which stays on the fp32 MFMA path: sentences/s, its FFN-up roofline
+    against the bf16 peak / 6, and the largest difference of its vectors from
+    the fp32 path's on this batch."""
+    cfg = spec.model
+    B, S = d_ids.shape
+    m = eb.Model.from_weights(weights, cfg, "fp32-bf16x6")
+    out = torch.empty_like(d_ref)
+    stream = torch.cuda.current_stream().cuda_stream
+    if not graph_replay:
+        m.set_graph_replay(False)
+
+    def step():
+        m.encode_device(d_ids.data_ptr(), d_mask.data_ptr(), B, S, out.data_ptr(), True, stream)
+
+    for _ in range(warmup):
+        step()
+    m.synchronize()
+    torch.cuda.synchronize()
+    times = []
+    t_all = time.perf_counter()
+    for _ in range(steps):
+        t0 = time.perf_counter()
+        step()
+        torch.cuda.synchronize()
+        times.append(time.perf_counter() - t0)
+    wall = time.perf_counter() - t_all
+    m.synchronize()
+    max_abs = float((out - d_ref).abs().max())
+    m.profile_enable(profile_kernel)
+    for _ in range(steps):
+        step()
+    m.synchronize()
+    torch.cuda.synchronize()
+    launches, prof_ms = m.profile_read()
+    m.profile_enable("none")
+    m.close()
+    work, bound, wunit = kernel_work(cfg, lengths, B, profile_kernel)
+    avg = prof_ms / max(launches, 1)
+    peak = PEAK_TFLOPS["fp32-bf16x6"] if bound == "mfma" else HBM_PEAK_GBS
+    achieved = work / (avg * 1e-3) / (1e12 if bound == "mfma" else 1e9)
+    return {"value": round(B * steps / wall, 2), "unit": "sentences/s",
+            "ms_per_step": round(1e3 * wall / steps, 4),
+            "p50_batch_latency_ms": round(float(np.median(times)) * 1e3, 4),
+            "max_abs_vs_fp32_path": max_abs,
+            "gemm_arithmetic": "fp32 operands split into three bf16 parts, six bf16 MFMA products "
+                               "per fp32 product, fp32 accumulate (EBH_DTYPE_F32_BF16X6)",
+            "roofline": {"kernel": profile_kernel, "bound": bound, "achieved": round(achieved, 3),
+                         "peak": round(peak, 1), "unit": "TFLOP/s" if bound == "mfma" else "GB/s",
+                         "frac": round(achieved / peak, 4), "avg_launch_ms": round(avg, 5),
+                         "launches": launches}}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=30)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--config", default="c3", choices=["c1", "c2", "c3", "c4", "c5"])
-    ap.add_argument("--dtype", default=None, help="fp32 | bf16 (default: the config's)")
+    ap.add_argument("--dtype", default=None, help="fp32 | bf16 | fp32-bf16x6 (default: the config's)")
+    ap.add_argument("--bf16x6-steps", type=int, default=None,
+                    help="fp32 configs: also time an EBH_DTYPE_F32_BF16X6 model (fp32 GEMM products "
+                         "from six bf16 MFMA products) for this many steps, reported under "
+                         "fp32_bf16x6 beside the headline (default: --steps; 0 disables)")
     ap.add_argument("--profile-kernel", default="gemm_ffn_up", choices=KERNELS)
     ap.add_argument("--cpu-budget", type=float, default=16.0,
                     help="seconds of CPU baseline work, split over its two builds (0 disables)")
@@ -293,7 +356,7 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "f32" if dtype == "fp32" else "bf16",
+        "dtype": {"fp32": "f32", "bf16": "bf16", "fp32-bf16x6": "f32 (bf16x6 GEMM products)"}[dtype],
         "data": "synthetic (seeded ids, random-init N(0,0.02) weights; no checkpoint offline)",
         "config": {"workload": f"{args.config}: {cfg.num_hidden_layers}L H{cfg.hidden_size} "
                                f"I{cfg.intermediate_size} heads{cfg.num_attention_heads} "
@@ -327,6 +390,11 @@ def main():
             dst.copy_(src)
         torch.cuda.synchronize()
         result["copy_probe_bytes"] = n * 4
+    x6_steps = args.steps if args.bf16x6_steps is None else args.bf16x6_steps
+    if dtype == "fp32" and x6_steps > 0:
+        result["fp32_bf16x6"] = split_product_run(eb, torch, spec, weights, d_ids, d_mask, d_out, lengths,
+                                                  x6_steps, args.warmup, args.profile_kernel,
+                                                  not args.no_graph_replay)
     if args.cpu_budget > 0:
         result["cpu_baseline"] = cpu_baseline(spec, weights, ids, mask, args.cpu_budget)
     print(json.dumps(result), flush=True)

@@ -24,6 +24,7 @@ EBH_ERR_HIP = -5
 EBH_ERR_RANGE = -6
 EBH_DTYPE_F32 = 0
 EBH_DTYPE_BF16 = 1
+EBH_DTYPE_F32_BF16X6 = 2
 NOALLOC_SCRATCH_BYTES = 128 << 20   # EBH_NOALLOC_SCRATCH_BYTES
 EPI_BIAS, EPI_BIAS_GELU, EPI_BIAS_RESID, EPI_NONE = 0, 1, 2, 3
 PROF = {"none": 0, "gemm_qkv": 1, "attention": 2, "gemm_out": 3, "gemm_ffn_up": 4,

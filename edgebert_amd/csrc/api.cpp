@@ -414,6 +414,7 @@ int enqueue_kernels(ebh_model* m, Workspace& w, const int* d_ids, const int* d_m
         a.M_dev = w.ntok;
         a.N = N;
         a.K = K;
+        a.split6 = m->dtype == EBH_DTYPE_F32_BF16X6;
         ProfPair p2{};
         bool on2 = false;
         prof_begin(m, prof_kind, kind, s, p2, on2);
@@ -475,6 +476,7 @@ int enqueue_kernels(ebh_model* m, Workspace& w, const int* d_ids, const int* d_m
         a.ln_g = g;
         a.ln_b = b;
         a.ln_eps = eps;
+        a.split6 = m->dtype == EBH_DTYPE_F32_BF16X6;
         ProfPair p2{};
         bool on2 = false;
         prof_begin(m, prof_kind, kind, s, p2, on2);
@@ -790,7 +792,7 @@ int ebh_finalize(ebh_model* m, int32_t dtype) {
     if (!m) return fail(EBH_ERR_INVALID_ARG, "null model");
     std::lock_guard<std::mutex> lk(m->mu);
     if (m->finalized) return fail(EBH_ERR_STATE, "model already finalized");
-    if (dtype != EBH_DTYPE_F32 && dtype != EBH_DTYPE_BF16)
+    if (dtype != EBH_DTYPE_F32 && dtype != EBH_DTYPE_BF16 && dtype != EBH_DTYPE_F32_BF16X6)
         return fail(EBH_ERR_INVALID_ARG, "unknown dtype %d", dtype);
     if (dtype == EBH_DTYPE_BF16 && (m->cfg.hidden_size % 64 || m->cfg.intermediate_size % 64 ||
                                     !ebh::row4_shape_ok(m->cfg.hidden_size)))
@@ -1274,7 +1276,7 @@ int ebh_op_gemm(const float* A, int64_t lda, const void* W, int64_t ldw, int32_t
     if (epilogue == EBH_EPI_BIAS_RESID && (!residual || ldr < N))
         return fail(EBH_ERR_INVALID_ARG, "residual epilogue needs a residual of row stride >= N");
     const int q = w_dtype == EBH_DTYPE_BF16 ? 8 : 4;
-    if (w_dtype != EBH_DTYPE_F32 && w_dtype != EBH_DTYPE_BF16)
+    if (w_dtype != EBH_DTYPE_F32 && w_dtype != EBH_DTYPE_BF16 && w_dtype != EBH_DTYPE_F32_BF16X6)
         return fail(EBH_ERR_INVALID_ARG, "unknown dtype %d", w_dtype);
     if (K % q || lda % 4 || ldw % q || lda < K || ldw < K || ldc < N)
         return fail(EBH_ERR_INVALID_ARG, "K and strides must be multiples of %d and cover the rows", q);
@@ -1283,6 +1285,7 @@ int ebh_op_gemm(const float* A, int64_t lda, const void* W, int64_t ldw, int32_t
     a.A = A; a.W = W; a.bias = bias; a.R = residual; a.C = C;
     a.lda = lda; a.ldw = ldw; a.ldr = ldr; a.ldc = ldc;
     a.M_max = M; a.M_dev = nullptr; a.N = N; a.K = K;
+    a.split6 = w_dtype == EBH_DTYPE_F32_BF16X6;
     hipStream_t s = static_cast<hipStream_t>(stream);
     hipError_t e = w_dtype == EBH_DTYPE_BF16 ? ebh::launch_gemm_bf16(a, epilogue, s)
                                               : ebh::launch_gemm_f32(a, epilogue, s);

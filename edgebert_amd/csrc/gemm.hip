@@ -276,8 +276,33 @@ constexpr int BUFFER_RSRC_WORD3 = 0x00020000;
 // and a lane holds four consecutive columns of one C row per group of four
 // accumulators (epilogue_packed).  LDS offsets below are in
 // 4-byte words, so both element types share the layout and the swizzle.
+// Eight fp32 values (x0, x1) split into three bf16 vectors with
+// x = h + m + l: h = bf16(x), m = bf16(x - h), l = bf16(x - h - m), each
+// rounded to nearest even; both differences are exact in fp32 (x - h has at
+// most 16 significant bits).  |x - h - m - l| <= 2^-26 |x| or so, and the
+// split products dropped by the six-product GEMM (m.l, l.m, l.l) are below
+// 2^-27 |a.b|.
+__device__ __forceinline__ void split3_bf16(const v4f& x0, const v4f& x1, v8bf& h, v8bf& m, v8bf& l) {
+    uint32_t hh[4], mm[4], ll[4];
+    const float xs[8] = {x0[0], x0[1], x0[2], x0[3], x1[0], x1[1], x1[2], x1[3]};
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        const float a = xs[2 * e], b = xs[2 * e + 1];
+        const uint32_t ph = pack_bf16x2(a, b);
+        const float ra = a - __uint_as_float(ph << 16), rb = b - __uint_as_float(ph & 0xffff0000u);
+        const uint32_t pm = pack_bf16x2(ra, rb);
+        const float sa = ra - __uint_as_float(pm << 16), sb = rb - __uint_as_float(pm & 0xffff0000u);
+        hh[e] = ph;
+        mm[e] = pm;
+        ll[e] = pack_bf16x2(sa, sb);
+    }
+    h = __builtin_bit_cast(v8bf, make_uint4(hh[0], hh[1], hh[2], hh[3]));
+    m = __builtin_bit_cast(v8bf, make_uint4(mm[0], mm[1], mm[2], mm[3]));
+    l = __builtin_bit_cast(v8bf, make_uint4(ll[0], ll[1], ll[2], ll[3]));
+}
+
 template <bool BF16, bool OUT16, int BM, int BN, int BK, int WAVES_M, int WAVES_N, int NSTAGE, int EPI,
-          bool SPREAD = BF16, bool PREFETCH = BF16>
+          bool SPREAD = BF16, bool PREFETCH = BF16, bool SPLIT6 = false>
 __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_persistent_kernel(GemmArgs p) {
     constexpr int ES = BF16 ? 2 : 4;              // bytes per element
     constexpr int EPC = 16 / ES;                  // elements per 16-byte chunk
@@ -754,6 +779,39 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_persistent_kernel
                 for (int j = 0; j < FN; ++j)
                     wfb[b][j] = *reinterpret_cast<const v4f*>(st + w_row + j * 32 * RW + ko);
             };
+            if constexpr (SPLIT6) {
+                static_assert(!BF16 && KS % 2 == 0, "split products: fp32 tiles of whole 16-deep slices");
+                // fp32 A and W fragments, split in registers into bf16 parts
+                // h + m + l; six bf16 MFMAs per block and 16-deep slice (the
+                // smallest products first).  Lane half h takes k = 16 sp +
+                // 8 h .. +7: fp32 chunks 4 sp + 2 h and 4 sp + 2 h + 1.
+#pragma unroll
+                for (int sp = 0; sp < KS / 2; ++sp) {
+                    const int c0 = 4 * sp + 2 * half;
+                    const int ko0 = 4 * (c0 ^ sw), ko1 = 4 * ((c0 + 1) ^ sw);
+                    v8bf wh[FN], wm[FN], wl[FN];
+#pragma unroll
+                    for (int j = 0; j < FN; ++j)
+                        split3_bf16(*reinterpret_cast<const v4f*>(st + w_row + j * 32 * RW + ko0),
+                                    *reinterpret_cast<const v4f*>(st + w_row + j * 32 * RW + ko1), wh[j], wm[j], wl[j]);
+#pragma unroll
+                    for (int i = 0; i < FM; ++i) {
+                        v8bf ah, am, al;
+                        split3_bf16(*reinterpret_cast<const v4f*>(st + a_row + i * 32 * RW + ko0),
+                                    *reinterpret_cast<const v4f*>(st + a_row + i * 32 * RW + ko1), ah, am, al);
+#pragma unroll
+                        for (int j = 0; j < FN; ++j) {
+                            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(al, wh[j], acc[i][j], 0, 0, 0);
+                            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(am, wm[j], acc[i][j], 0, 0, 0);
+                            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah, wl[j], acc[i][j], 0, 0, 0);
+                            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(am, wh[j], acc[i][j], 0, 0, 0);
+                            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah, wm[j], acc[i][j], 0, 0, 0);
+                            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah, wh[j], acc[i][j], 0, 0, 0);
+                        }
+                    }
+                }
+                continue;
+            }
             if (PREF) rd(0, 0);
 #pragma unroll
             for (int s = 0; s < KS; ++s) {
@@ -1101,8 +1159,18 @@ int device_cu_count() {
 
 static int cu_count() { return device_cu_count(); }
 
+template <int BM, int BN, int BK, int WAVES_M, int WAVES_N, int NSTAGE, bool BF16, bool OUT16, bool SPLIT6>
+static hipError_t launch_persistent_kernel(const GemmArgs& a, int epi, hipStream_t s, int wg_per_cu);
+
 template <int BM, int BN, int BK, int WAVES_M, int WAVES_N, int NSTAGE, bool BF16 = false, bool OUT16 = false>
 static hipError_t launch_persistent(const GemmArgs& a, int epi, hipStream_t s, int wg_per_cu = 1) {
+    if constexpr (!BF16 && (BK / 4) % 4 == 0)
+        if (a.split6) return launch_persistent_kernel<BM, BN, BK, WAVES_M, WAVES_N, NSTAGE, false, OUT16, true>(a, epi, s, wg_per_cu);
+    return launch_persistent_kernel<BM, BN, BK, WAVES_M, WAVES_N, NSTAGE, BF16, OUT16, false>(a, epi, s, wg_per_cu);
+}
+
+template <int BM, int BN, int BK, int WAVES_M, int WAVES_N, int NSTAGE, bool BF16, bool OUT16, bool SPLIT6>
+static hipError_t launch_persistent_kernel(const GemmArgs& a, int epi, hipStream_t s, int wg_per_cu) {
     // One work item per tile and k-split.
     const int64_t items = (int64_t)((a.M_max + BM - 1) / BM) * ((a.N + BN - 1) / BN) * (a.splits > 1 ? a.splits : 1);
     if (items == 0) return hipSuccess;
@@ -1110,13 +1178,13 @@ static hipError_t launch_persistent(const GemmArgs& a, int epi, hipStream_t s, i
     const dim3 block(64 * WAVES_M * WAVES_N);
     switch (epi) {
         case EPI_BIAS:
-            hipLaunchKernelGGL((gemm_persistent_kernel<BF16, OUT16, BM, BN, BK, WAVES_M, WAVES_N, NSTAGE, EPI_BIAS>), dim3(grid), block, 0, s, a);
+            hipLaunchKernelGGL((gemm_persistent_kernel<BF16, OUT16, BM, BN, BK, WAVES_M, WAVES_N, NSTAGE, EPI_BIAS, BF16, BF16, SPLIT6>), dim3(grid), block, 0, s, a);
             break;
         case EPI_BIAS_GELU:
-            hipLaunchKernelGGL((gemm_persistent_kernel<BF16, OUT16, BM, BN, BK, WAVES_M, WAVES_N, NSTAGE, EPI_BIAS_GELU>), dim3(grid), block, 0, s, a);
+            hipLaunchKernelGGL((gemm_persistent_kernel<BF16, OUT16, BM, BN, BK, WAVES_M, WAVES_N, NSTAGE, EPI_BIAS_GELU, BF16, BF16, SPLIT6>), dim3(grid), block, 0, s, a);
             break;
         case EPI_NONE:
-            hipLaunchKernelGGL((gemm_persistent_kernel<BF16, OUT16, BM, BN, BK, WAVES_M, WAVES_N, NSTAGE, EPI_NONE>), dim3(grid), block, 0, s, a);
+            hipLaunchKernelGGL((gemm_persistent_kernel<BF16, OUT16, BM, BN, BK, WAVES_M, WAVES_N, NSTAGE, EPI_NONE, BF16, BF16, SPLIT6>), dim3(grid), block, 0, s, a);
             break;
         default:
             return hipErrorInvalidValue;
@@ -1233,8 +1301,13 @@ hipError_t launch_gemm_f32_add_ln(const GemmArgs& a, hipStream_t s) {
     const int tiles = (a.M_max + ADD_LN_BM - 1) / ADD_LN_BM;
     if (tiles == 0) return hipSuccess;
     const int grid = std::min(tiles, cu_count());
-    hipLaunchKernelGGL((gemm_persistent_kernel<false, false, ADD_LN_BM, ADD_LN_BN, ADD_LN_BK, 2, 4, 2, EPI_ADD_LN>),
-                       dim3(grid), dim3(512), 0, s, a);
+    if (a.split6)
+        hipLaunchKernelGGL((gemm_persistent_kernel<false, false, ADD_LN_BM, ADD_LN_BN, ADD_LN_BK, 2, 4, 2, EPI_ADD_LN,
+                                                   false, false, true>),
+                           dim3(grid), dim3(512), 0, s, a);
+    else
+        hipLaunchKernelGGL((gemm_persistent_kernel<false, false, ADD_LN_BM, ADD_LN_BN, ADD_LN_BK, 2, 4, 2, EPI_ADD_LN>),
+                           dim3(grid), dim3(512), 0, s, a);
     return hipGetLastError();
 }
 

@@ -29,6 +29,13 @@ struct GemmArgs {
     const float* ln_g;
     const float* ln_b;
     float ln_eps;
+    // fp32 products as six bf16 MFMA products (the persistent kernels; other
+    // paths ignore it): each fp32 operand is split in registers into three
+    // bf16 parts h + m + l (round to nearest even at each step), and
+    // a.b = ah.bh + ah.bm + am.bh + ah.bl + am.bm + al.bh, every product
+    // exact in fp32, accumulated in fp32 (the dropped terms are below 2^-27
+    // of |a.b|).
+    int split6;
 };
 
 // The few-token GEMM path: M_max <= SKINNY_MAX_ROWS rows in 16-row blocks,

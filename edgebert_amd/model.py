@@ -35,7 +35,10 @@ from . import _native as N
 from .synth import BertConfig
 from .tokenizer import Tokenizer, c_texts, hf_encode_batch_ids, hf_tokenizer
 
-_DTYPES = {"fp32": N.EBH_DTYPE_F32, "f32": N.EBH_DTYPE_F32, "bf16": N.EBH_DTYPE_BF16}
+# "fp32-bf16x6": an fp32 model whose GEMMs form each fp32 product from six
+# bf16 MFMA products of three-way bf16 splits (include/edgebert_hip.h).
+_DTYPES = {"fp32": N.EBH_DTYPE_F32, "f32": N.EBH_DTYPE_F32, "bf16": N.EBH_DTYPE_BF16,
+           "fp32-bf16x6": N.EBH_DTYPE_F32_BF16X6}
 
 
 def _ptr(a: np.ndarray):

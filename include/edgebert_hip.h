@@ -42,6 +42,16 @@ extern "C" {
 
 #define EBH_DTYPE_F32 0  /* fp32 GEMMs (parity path)                          */
 #define EBH_DTYPE_BF16 1 /* bf16 GEMM inputs, fp32 accumulate; LN/softmax fp32 */
+/* fp32 model (fp32 weights and activations, everything else as EBH_DTYPE_F32)
+ * whose GEMMs form each fp32 product from bf16 MFMA products: both operands
+ * are split in registers into three bf16 parts (h + m + l, round to nearest
+ * even) and a.b = ah.bh + ah.bm + am.bh + ah.bl + am.bm + al.bh, each product
+ * exact in fp32, accumulated in fp32; the terms left out are below 2^-27 of
+ * |a.b|.  Measured against fp64 its GEMM errors are no larger than the fp32
+ * MFMA path's; its large GEMMs run faster (bf16 matrix rate is 16x fp32's).
+ * Products of at most 64 rows keep the fp32 kernels.  Not in the reference:
+ * an opt-in for callers that want the fp32 path's accuracy at more speed. */
+#define EBH_DTYPE_F32_BF16X6 2
 
 typedef struct ebh_model ebh_model;
 

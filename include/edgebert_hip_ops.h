@@ -30,7 +30,9 @@ extern "C" {
  * 732-733, 741-747, 673, 678, 958-978), batch folded into M:
  * A [M, K] fp32 (row stride lda), W [N, K] HF layout (row stride ldw), fp32
  * when w_dtype == EBH_DTYPE_F32 or bf16 bits (uint16) when EBH_DTYPE_BF16 (A
- * is then rounded to bf16 on load; accumulation is fp32).  C [M, N] (ldc);
+ * is then rounded to bf16 on load; accumulation is fp32); w_dtype
+ * EBH_DTYPE_F32_BF16X6: fp32 W, products formed as six bf16 MFMA products of
+ * three-way bf16 splits of A and W (see edgebert_hip.h).  C [M, N] (ldc);
  * residual [M, N] (ldr) only for EBH_EPI_BIAS_RESID; bias may be NULL for EBH_EPI_NONE.  K and the strides must
  * be multiples of 4 (fp32) / 8 (bf16). */
 EBH_API int ebh_op_gemm(const float* A, int64_t lda, const void* W, int64_t ldw, int32_t w_dtype,

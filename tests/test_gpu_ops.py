@@ -110,6 +110,38 @@ def test_gemm_f32_dispatch_paths(env, M, N, K, epi):
     np.testing.assert_allclose(dC.cpu().numpy(), want, rtol=0, atol=tol)
 
 
+@pytest.mark.parametrize("M,N,K,epi", [
+    (4100, 1152, 384, 0), (8192, 384, 1536, 3), (33000, 1536, 384, 1), (32768, 1152, 384, 0),
+    (20000, 1152, 384, 1), (40000, 576, 256, 3), (40000, 512, 160, 3), (9000, 1024, 384, 1),
+    (500, 256, 96, 0), (2000, 384, 1536, 3)])
+def test_gemm_f32_split_products(env, M, N, K, epi):
+    """EBH_DTYPE_F32_BF16X6: fp32 products formed from six bf16 MFMA products
+    of three-way bf16 splits, on every tile configuration of the fp32
+    dispatch.  Against the float64 product it meets the fp32 tolerance, and
+    its largest error is at most that of the fp32 MFMA path on the same data
+    (times 1.5, for the different summation order)."""
+    torch, eb, Nn, L = env
+    rng = np.random.default_rng(M + N + K + 7)
+    A = rng.standard_normal((M, K)).astype(np.float32)
+    W = (0.05 * rng.standard_normal((N, K))).astype(np.float32)
+    bias = rng.standard_normal(N).astype(np.float32)
+    dA, dW, db = dev(torch, A), dev(torch, W), dev(torch, bias)
+    want = A.astype(np.float64) @ W.T.astype(np.float64) + (bias if epi != 3 else 0.0)
+    if epi == 1:
+        want = gelu64(want)
+    errs = {}
+    for wd in (Nn.EBH_DTYPE_F32, Nn.EBH_DTYPE_F32_BF16X6):
+        dC = torch.full((M, N), float("nan"), device="cuda")
+        Nn.check(L.ebh_op_gemm(vp(dA), K, vp(dW), K, wd, vp(db) if epi != 3 else None,
+                               None, N, vp(dC), N, M, N, K, epi, stream(torch)))
+        torch.cuda.synchronize()
+        errs[wd] = float(np.abs(dC.cpu().numpy() - want).max())
+    tol = 2e-6 * np.sqrt(K) * (np.abs(A).max() * np.abs(W).max() * np.sqrt(K)) + 1e-5
+    print(f"max |err| fp32 MFMA {errs[Nn.EBH_DTYPE_F32]:.3e}, bf16x6 {errs[Nn.EBH_DTYPE_F32_BF16X6]:.3e}", flush=True)
+    assert errs[Nn.EBH_DTYPE_F32_BF16X6] <= tol
+    assert errs[Nn.EBH_DTYPE_F32_BF16X6] <= 1.5 * errs[Nn.EBH_DTYPE_F32] + 1e-7
+
+
 @pytest.mark.parametrize("M,N,K", [(1, 32, 64), (16, 1152, 384), (33, 384, 1536), (64, 3072, 768),
                                    (50, 96, 192), (7, 64, 320)])
 @pytest.mark.parametrize("epi", [0, 1, 3])

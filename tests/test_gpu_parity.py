@@ -62,6 +62,22 @@ def test_encode_matches_unpadded_oracle(eb, oracle_mod, weights_for, cname):
     assert np.array_equal(cu, np.concatenate([[0], np.cumsum(lengths)]).astype(np.int32))
 
 
+@pytest.mark.parametrize("cname", ["c2", "c3", "c4"])
+def test_split_product_gemms_match_unpadded_oracle(eb, oracle_mod, weights_for, cname):
+    """An EBH_DTYPE_F32_BF16X6 model (fp32 GEMM products from six bf16 MFMA
+    products) holds the fp32 bars against the oracle's unpadded run (c3: a
+    16-sequence subsample of the full batch)."""
+    spec = eb.CONFIGS[cname]
+    w = weights_for(spec.model)
+    ids, mask, lengths = eb.make_inputs(spec)
+    m = gpu_model(eb, spec.model, w, "fp32-bf16x6")
+    got = m.encode_ids(ids, mask, normalize=True)
+    sel = np.arange(spec.batch) if cname != "c3" else np.arange(5, spec.batch, spec.batch // 16)[:16]
+    want = oracle_mod.OracleModel(spec.model, w).encode_unpadded(ids[sel], mask[sel], normalize=True)
+    err, cos = _report(f"{cname} fp32-bf16x6 vs unpadded oracle", got[sel], want)
+    assert err <= FP32_MAX_ABS and cos >= FP32_MIN_COS
+
+
 @pytest.mark.parametrize("cname", ["c1", "c2"])
 def test_forward_matches_padded_oracle(eb, oracle_mod, weights_for, cname):
     """Model::forward on the reference's f32 arrays vs the oracle's padded run."""
