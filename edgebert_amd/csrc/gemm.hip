@@ -404,7 +404,7 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_persistent_kernel
     // loads too little time to land before the next k-tile's wait.  Part
     // `part` of NPART issues loads [part * PER, (part + 1) * PER); the last
     // part adds the bias chunk and moves on to the next k-tile.
-    constexpr int NPART = SPREAD && KS > 1 ? KS / 2 : 1;
+    constexpr int NPART = SPREAD && KS > 1 ? KS / 2 : 1;   // SPLIT6: one part per 16-deep slice
     constexpr int PER = (NL + NPART - 1) / NPART;
     auto issue_part = [&](int part) {
         float* st = smem + (nit % NSTAGE) * STAGE;
@@ -787,6 +787,7 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_persistent_kernel
                 // 8 h .. +7: fp32 chunks 4 sp + 2 h and 4 sp + 2 h + 1.
 #pragma unroll
                 for (int sp = 0; sp < KS / 2; ++sp) {
+                    if (SPREAD && refill && sp < NPART) issue_part(sp);
                     const int c0 = 4 * sp + 2 * half;
                     const int ko0 = 4 * (c0 ^ sw), ko1 = 4 * ((c0 + 1) ^ sw);
                     v8bf wh[FN], wm[FN], wl[FN];
@@ -1178,13 +1179,13 @@ static hipError_t launch_persistent_kernel(const GemmArgs& a, int epi, hipStream
     const dim3 block(64 * WAVES_M * WAVES_N);
     switch (epi) {
         case EPI_BIAS:
-            hipLaunchKernelGGL((gemm_persistent_kernel<BF16, OUT16, BM, BN, BK, WAVES_M, WAVES_N, NSTAGE, EPI_BIAS, BF16, BF16, SPLIT6>), dim3(grid), block, 0, s, a);
+            hipLaunchKernelGGL((gemm_persistent_kernel<BF16, OUT16, BM, BN, BK, WAVES_M, WAVES_N, NSTAGE, EPI_BIAS, BF16 || SPLIT6, BF16, SPLIT6>), dim3(grid), block, 0, s, a);
             break;
         case EPI_BIAS_GELU:
-            hipLaunchKernelGGL((gemm_persistent_kernel<BF16, OUT16, BM, BN, BK, WAVES_M, WAVES_N, NSTAGE, EPI_BIAS_GELU, BF16, BF16, SPLIT6>), dim3(grid), block, 0, s, a);
+            hipLaunchKernelGGL((gemm_persistent_kernel<BF16, OUT16, BM, BN, BK, WAVES_M, WAVES_N, NSTAGE, EPI_BIAS_GELU, BF16 || SPLIT6, BF16, SPLIT6>), dim3(grid), block, 0, s, a);
             break;
         case EPI_NONE:
-            hipLaunchKernelGGL((gemm_persistent_kernel<BF16, OUT16, BM, BN, BK, WAVES_M, WAVES_N, NSTAGE, EPI_NONE, BF16, BF16, SPLIT6>), dim3(grid), block, 0, s, a);
+            hipLaunchKernelGGL((gemm_persistent_kernel<BF16, OUT16, BM, BN, BK, WAVES_M, WAVES_N, NSTAGE, EPI_NONE, BF16 || SPLIT6, BF16, SPLIT6>), dim3(grid), block, 0, s, a);
             break;
         default:
             return hipErrorInvalidValue;
@@ -1303,7 +1304,7 @@ hipError_t launch_gemm_f32_add_ln(const GemmArgs& a, hipStream_t s) {
     const int grid = std::min(tiles, cu_count());
     if (a.split6)
         hipLaunchKernelGGL((gemm_persistent_kernel<false, false, ADD_LN_BM, ADD_LN_BN, ADD_LN_BK, 2, 4, 2, EPI_ADD_LN,
-                                                   false, false, true>),
+                                                   true, false, true>),
                            dim3(grid), dim3(512), 0, s, a);
     else
         hipLaunchKernelGGL((gemm_persistent_kernel<false, false, ADD_LN_BM, ADD_LN_BN, ADD_LN_BK, 2, 4, 2, EPI_ADD_LN>),
