@@ -433,6 +433,14 @@ __global__ __launch_bounds__(256) void embed_ln4_kernel(
 // 8 * (c * LPR + sub) .. +7 (H == 8 * NV8 * LPR), so the bf16 product, the
 // bf16 residual and the bf16 result move as uint4 (a wave instruction moves
 // 1 KB).  x16 = bf16(LayerNorm((y + bias) + x16)), sums and statistics fp32.
+// Each lane group takes RPG rows (rows g, g + RPB, ... of the workgroup's
+// block, so every step of the workgroup covers RPB consecutive rows): bias,
+// gamma and beta are loaded once for all of them (they are 72 floats a lane,
+// 3x the row's own bytes, and would otherwise load again per row through the
+// CU's load path), and the next row's product and residual are loaded before
+// the current row's sums.
+constexpr int LN8_RPG = 4;
+
 template <int NV8, int LPR>
 __global__ __launch_bounds__(256) void add_layernorm8_b16_kernel(const uint16_t* __restrict__ y,
                                                                  const float* __restrict__ bias,
@@ -440,18 +448,14 @@ __global__ __launch_bounds__(256) void add_layernorm8_b16_kernel(const uint16_t*
                                                                  const float* __restrict__ bta, int rows_max,
                                                                  const int* rows_dev, int H, float eps) {
     constexpr int RPB = 256 / LPR;
-    const int row = blockIdx.x * RPB + threadIdx.x / LPR, sub = threadIdx.x % LPR;
+    const int grp = threadIdx.x / LPR, sub = threadIdx.x % LPR;
+    const int row0 = blockIdx.x * RPB * LN8_RPG + grp;
     const int rows = rows_dev ? *rows_dev : rows_max;
-    if (row >= rows) return;
-    const uint16_t* yr = y + (int64_t)row * H;
-    uint16_t* xr = x16 + (int64_t)row * H;
-    uint4 ya[NV8], xa[NV8];
+    if (row0 >= rows) return;
     float4 bb[NV8][2], g4[NV8][2], b4[NV8][2];
 #pragma unroll
     for (int c = 0; c < NV8; ++c) {
         const int i = 8 * (c * LPR + sub);
-        ya[c] = *reinterpret_cast<const uint4*>(yr + i);
-        xa[c] = *reinterpret_cast<const uint4*>(xr + i);
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
             bb[c][h] = *reinterpret_cast<const float4*>(bias + i + 4 * h);
@@ -461,44 +465,61 @@ __global__ __launch_bounds__(256) void add_layernorm8_b16_kernel(const uint16_t*
     }
     auto lo = [](uint32_t w) { return __uint_as_float(w << 16); };
     auto hi = [](uint32_t w) { return __uint_as_float(w & 0xFFFF0000u); };
-    float v[NV8][8];
-    float s = 0.0f;
+    uint4 ya[NV8], xa[NV8];
+    auto load_row = [&](int row) __attribute__((always_inline)) {
 #pragma unroll
-    for (int c = 0; c < NV8; ++c) {
-        const uint32_t yw[4] = {ya[c].x, ya[c].y, ya[c].z, ya[c].w};
-        const uint32_t xw[4] = {xa[c].x, xa[c].y, xa[c].z, xa[c].w};
-        const float bv[8] = {bb[c][0].x, bb[c][0].y, bb[c][0].z, bb[c][0].w,
-                             bb[c][1].x, bb[c][1].y, bb[c][1].z, bb[c][1].w};
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            v[c][2 * e] = (lo(yw[e]) + bv[2 * e]) + lo(xw[e]);
-            v[c][2 * e + 1] = (hi(yw[e]) + bv[2 * e + 1]) + hi(xw[e]);
+        for (int c = 0; c < NV8; ++c) {
+            const int i = 8 * (c * LPR + sub);
+            ya[c] = *reinterpret_cast<const uint4*>(y + (int64_t)row * H + i);
+            xa[c] = *reinterpret_cast<const uint4*>(x16 + (int64_t)row * H + i);
         }
+    };
+    load_row(row0);
 #pragma unroll
-        for (int e = 0; e < 8; e += 2) s += v[c][e] + v[c][e + 1];
-    }
-    const float mean = group_sum<LPR>(s) / (float)H;
-    float ss = 0.0f;
+    for (int r = 0; r < LN8_RPG; ++r) {
+        const int row = row0 + r * RPB;
+        if (row >= rows) break;  // uniform over the row's lane group
+        float v[NV8][8];
+        float s = 0.0f;
 #pragma unroll
-    for (int c = 0; c < NV8; ++c)
+        for (int c = 0; c < NV8; ++c) {
+            const uint32_t yw[4] = {ya[c].x, ya[c].y, ya[c].z, ya[c].w};
+            const uint32_t xw[4] = {xa[c].x, xa[c].y, xa[c].z, xa[c].w};
+            const float bv[8] = {bb[c][0].x, bb[c][0].y, bb[c][0].z, bb[c][0].w,
+                                 bb[c][1].x, bb[c][1].y, bb[c][1].z, bb[c][1].w};
 #pragma unroll
-        for (int e = 0; e < 8; e += 2) {
-            const float d0 = v[c][e] - mean, d1 = v[c][e + 1] - mean;
-            ss += d0 * d0 + d1 * d1;
+            for (int e = 0; e < 4; ++e) {
+                v[c][2 * e] = (lo(yw[e]) + bv[2 * e]) + lo(xw[e]);
+                v[c][2 * e + 1] = (hi(yw[e]) + bv[2 * e + 1]) + hi(xw[e]);
+            }
+#pragma unroll
+            for (int e = 0; e < 8; e += 2) s += v[c][e] + v[c][e + 1];
         }
-    const float inv_std = 1.0f / sqrtf(group_sum<LPR>(ss) / (float)H + eps);
+        if (r + 1 < LN8_RPG && row + RPB < rows) load_row(row + RPB);
+        const float mean = group_sum<LPR>(s) / (float)H;
+        float ss = 0.0f;
 #pragma unroll
-    for (int c = 0; c < NV8; ++c) {
-        const float gv[8] = {g4[c][0].x, g4[c][0].y, g4[c][0].z, g4[c][0].w,
-                             g4[c][1].x, g4[c][1].y, g4[c][1].z, g4[c][1].w};
-        const float tv[8] = {b4[c][0].x, b4[c][0].y, b4[c][0].z, b4[c][0].w,
-                             b4[c][1].x, b4[c][1].y, b4[c][1].z, b4[c][1].w};
-        uint32_t o[4];
+        for (int c = 0; c < NV8; ++c)
 #pragma unroll
-        for (int e = 0; e < 4; ++e)
-            o[e] = pack_bf16x2((v[c][2 * e] - mean) * inv_std * gv[2 * e] + tv[2 * e],
-                               (v[c][2 * e + 1] - mean) * inv_std * gv[2 * e + 1] + tv[2 * e + 1]);
-        *reinterpret_cast<uint4*>(xr + 8 * (c * LPR + sub)) = make_uint4(o[0], o[1], o[2], o[3]);
+            for (int e = 0; e < 8; e += 2) {
+                const float d0 = v[c][e] - mean, d1 = v[c][e + 1] - mean;
+                ss += d0 * d0 + d1 * d1;
+            }
+        const float inv_std = 1.0f / sqrtf(group_sum<LPR>(ss) / (float)H + eps);
+        uint16_t* xr = x16 + (int64_t)row * H;
+#pragma unroll
+        for (int c = 0; c < NV8; ++c) {
+            const float gv[8] = {g4[c][0].x, g4[c][0].y, g4[c][0].z, g4[c][0].w,
+                                 g4[c][1].x, g4[c][1].y, g4[c][1].z, g4[c][1].w};
+            const float tv[8] = {b4[c][0].x, b4[c][0].y, b4[c][0].z, b4[c][0].w,
+                                 b4[c][1].x, b4[c][1].y, b4[c][1].z, b4[c][1].w};
+            uint32_t o[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+                o[e] = pack_bf16x2((v[c][2 * e] - mean) * inv_std * gv[2 * e] + tv[2 * e],
+                                   (v[c][2 * e + 1] - mean) * inv_std * gv[2 * e + 1] + tv[2 * e + 1]);
+            *reinterpret_cast<uint4*>(xr + 8 * (c * LPR + sub)) = make_uint4(o[0], o[1], o[2], o[3]);
+        }
     }
 }
 
@@ -609,7 +630,8 @@ hipError_t launch_add_layernorm_y16(const uint16_t* y, const float* bias, float*
     row8_shape(H, lpr8, nv8);
     if (!x && lpr8 && ((uintptr_t)y & 15) == 0 && ((uintptr_t)x16 & 15) == 0 && ((uintptr_t)g & 15) == 0 &&
         ((uintptr_t)b & 15) == 0 && ((uintptr_t)bias & 15) == 0) {
-        const dim3 grid8((rows_max + 256 / lpr8 - 1) / (256 / lpr8));
+        const int rows_per_wg = 256 / lpr8 * LN8_RPG;
+        const dim3 grid8((rows_max + rows_per_wg - 1) / rows_per_wg);
 #define EBH_LN8(L, N)                                                                                  \
         if (lpr8 == L && nv8 == N) {                                                                    \
             hipLaunchKernelGGL((add_layernorm8_b16_kernel<N, L>), grid8, dim3(256), 0, s, y, bias, x16, g, b, \
