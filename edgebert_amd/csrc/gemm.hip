@@ -302,7 +302,7 @@ __device__ __forceinline__ void split3_bf16(const v4f& x0, const v4f& x1, v8bf& 
 }
 
 template <bool BF16, bool OUT16, int BM, int BN, int BK, int WAVES_M, int WAVES_N, int NSTAGE, int EPI,
-          bool SPREAD = BF16, bool PREFETCH = BF16, bool SPLIT6 = false>
+          bool PREFETCH = BF16, bool SPLIT6 = false>
 __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_persistent_kernel(GemmArgs p) {
     constexpr int ES = BF16 ? 2 : 4;              // bytes per element
     constexpr int EPC = 16 / ES;                  // elements per 16-byte chunk
@@ -395,16 +395,17 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_persistent_kernel
     };
     // Load instructions of k-tile j (the bias chunk rides with a tile's first k-tile).
     auto n_issued = [&](int j) { return NL + (HAS_BIAS && j % nk == 0 ? 1 : 0); };
-    // The loads of a k-tile go out in parts: all at once, or (SPREAD) one part
-    // before each of the first half of the k-slices' MFMAs.  The CU's vector
-    // memory path takes one 1 KB load per 16 cycles, and a wave stalls at
-    // issue while it is backed up; at bf16 rates a k-tile's loads need half of
-    // its MFMA time on that path, so one burst after the barrier would idle
-    // the MFMA pipes, while parts spread over all k-slices leave the last
-    // loads too little time to land before the next k-tile's wait.  Part
-    // `part` of NPART issues loads [part * PER, (part + 1) * PER); the last
-    // part adds the bias chunk and moves on to the next k-tile.
-    constexpr int NPART = SPREAD && KS > 1 ? KS / 2 : 1;   // SPLIT6: one part per 16-deep slice
+    // The loads of a k-tile go out in parts, one before each of the first
+    // half of its k-slices' MFMAs (split products: one per 16-deep slice).
+    // The CU's vector memory path takes one 1 KB load per 16 cycles, and a
+    // wave stalls at issue while it is backed up: one burst after the barrier
+    // would idle the MFMA pipes (at bf16 rates a k-tile's loads need half of
+    // its MFMA time on that path), while parts spread over all k-slices leave
+    // the last loads too little time to land before the next k-tile's wait
+    // (fp32 c3 forward 6.115 -> 6.043 ms against the burst).  Part `part` of
+    // NPART issues loads [part * PER, (part + 1) * PER); the last part adds the
+    // bias chunk and moves on to the next k-tile.
+    constexpr int NPART = KS > 1 ? KS / 2 : 1;
     constexpr int PER = (NL + NPART - 1) / NPART;
     auto issue_part = [&](int part) {
         float* st = smem + (nit % NSTAGE) * STAGE;
@@ -763,7 +764,6 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_persistent_kernel
                         for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
             }
             const bool refill = nit < total;
-            if (!SPREAD && refill) issue();
             const float* st = smem + (it % NSTAGE) * STAGE;
             // PREFETCH: k-slice s + 1's fragments are read while slice s's
             // MFMAs run (two fragment sets in registers); otherwise each
@@ -787,7 +787,7 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_persistent_kernel
                 // 8 h .. +7: fp32 chunks 4 sp + 2 h and 4 sp + 2 h + 1.
 #pragma unroll
                 for (int sp = 0; sp < KS / 2; ++sp) {
-                    if (SPREAD && refill && sp < NPART) issue_part(sp);
+                    if (refill && sp < NPART) issue_part(sp);
                     const int c0 = 4 * sp + 2 * half;
                     const int ko0 = 4 * (c0 ^ sw), ko1 = 4 * ((c0 + 1) ^ sw);
                     v8bf wh[FN], wm[FN], wl[FN];
@@ -816,7 +816,7 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_persistent_kernel
             if (PREF) rd(0, 0);
 #pragma unroll
             for (int s = 0; s < KS; ++s) {
-                if (SPREAD && refill && s < NPART) issue_part(s);
+                if (refill && s < NPART) issue_part(s);
                 if (!PREF) rd(s, 0);
                 else if (s + 1 < KS) rd(s + 1, (s + 1) & 1);
                 const v4f (&af)[FM] = afb[PREF ? (s & 1) : 0];
@@ -1179,13 +1179,13 @@ static hipError_t launch_persistent_kernel(const GemmArgs& a, int epi, hipStream
     const dim3 block(64 * WAVES_M * WAVES_N);
     switch (epi) {
         case EPI_BIAS:
-            hipLaunchKernelGGL((gemm_persistent_kernel<BF16, OUT16, BM, BN, BK, WAVES_M, WAVES_N, NSTAGE, EPI_BIAS, BF16 || SPLIT6, BF16, SPLIT6>), dim3(grid), block, 0, s, a);
+            hipLaunchKernelGGL((gemm_persistent_kernel<BF16, OUT16, BM, BN, BK, WAVES_M, WAVES_N, NSTAGE, EPI_BIAS, BF16, SPLIT6>), dim3(grid), block, 0, s, a);
             break;
         case EPI_BIAS_GELU:
-            hipLaunchKernelGGL((gemm_persistent_kernel<BF16, OUT16, BM, BN, BK, WAVES_M, WAVES_N, NSTAGE, EPI_BIAS_GELU, BF16 || SPLIT6, BF16, SPLIT6>), dim3(grid), block, 0, s, a);
+            hipLaunchKernelGGL((gemm_persistent_kernel<BF16, OUT16, BM, BN, BK, WAVES_M, WAVES_N, NSTAGE, EPI_BIAS_GELU, BF16, SPLIT6>), dim3(grid), block, 0, s, a);
             break;
         case EPI_NONE:
-            hipLaunchKernelGGL((gemm_persistent_kernel<BF16, OUT16, BM, BN, BK, WAVES_M, WAVES_N, NSTAGE, EPI_NONE, BF16 || SPLIT6, BF16, SPLIT6>), dim3(grid), block, 0, s, a);
+            hipLaunchKernelGGL((gemm_persistent_kernel<BF16, OUT16, BM, BN, BK, WAVES_M, WAVES_N, NSTAGE, EPI_NONE, BF16, SPLIT6>), dim3(grid), block, 0, s, a);
             break;
         default:
             return hipErrorInvalidValue;
@@ -1304,7 +1304,7 @@ hipError_t launch_gemm_f32_add_ln(const GemmArgs& a, hipStream_t s) {
     const int grid = std::min(tiles, cu_count());
     if (a.split6)
         hipLaunchKernelGGL((gemm_persistent_kernel<false, false, ADD_LN_BM, ADD_LN_BN, ADD_LN_BK, 2, 4, 2, EPI_ADD_LN,
-                                                   true, false, true>),
+                                                   false, true>),
                            dim3(grid), dim3(512), 0, s, a);
     else
         hipLaunchKernelGGL((gemm_persistent_kernel<false, false, ADD_LN_BM, ADD_LN_BN, ADD_LN_BK, 2, 4, 2, EPI_ADD_LN>),
