@@ -302,7 +302,7 @@ __device__ __forceinline__ void split3_bf16(const v4f& x0, const v4f& x1, v8bf& 
 }
 
 template <bool BF16, bool OUT16, int BM, int BN, int BK, int WAVES_M, int WAVES_N, int NSTAGE, int EPI,
-          bool PREFETCH = BF16, bool SPLIT6 = false>
+          bool SPLIT6 = false>
 __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_persistent_kernel(GemmArgs p) {
     constexpr int ES = BF16 ? 2 : 4;              // bytes per element
     constexpr int EPC = 16 / ES;                  // elements per 16-byte chunk
@@ -765,10 +765,10 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_persistent_kernel
             }
             const bool refill = nit < total;
             const float* st = smem + (it % NSTAGE) * STAGE;
-            // PREFETCH: k-slice s + 1's fragments are read while slice s's
-            // MFMAs run (two fragment sets in registers); otherwise each
-            // slice reads its own just before its MFMAs.
-            constexpr bool PREF = PREFETCH && KS > 1;
+            // k-slice s + 1's fragments are read while slice s's MFMAs run
+            // (two fragment sets in registers).  fp32 c3 forward 6.04 ->
+            // 6.00 ms against reading each slice's just before its MFMAs.
+            constexpr bool PREF = KS > 1;
             v4f afb[PREF ? 2 : 1][FM], wfb[PREF ? 2 : 1][FN];
             auto rd = [&](int s, int b) __attribute__((always_inline)) {
                 const int ko = 4 * ((2 * s + half) ^ sw);
@@ -1179,13 +1179,13 @@ static hipError_t launch_persistent_kernel(const GemmArgs& a, int epi, hipStream
     const dim3 block(64 * WAVES_M * WAVES_N);
     switch (epi) {
         case EPI_BIAS:
-            hipLaunchKernelGGL((gemm_persistent_kernel<BF16, OUT16, BM, BN, BK, WAVES_M, WAVES_N, NSTAGE, EPI_BIAS, BF16, SPLIT6>), dim3(grid), block, 0, s, a);
+            hipLaunchKernelGGL((gemm_persistent_kernel<BF16, OUT16, BM, BN, BK, WAVES_M, WAVES_N, NSTAGE, EPI_BIAS, SPLIT6>), dim3(grid), block, 0, s, a);
             break;
         case EPI_BIAS_GELU:
-            hipLaunchKernelGGL((gemm_persistent_kernel<BF16, OUT16, BM, BN, BK, WAVES_M, WAVES_N, NSTAGE, EPI_BIAS_GELU, BF16, SPLIT6>), dim3(grid), block, 0, s, a);
+            hipLaunchKernelGGL((gemm_persistent_kernel<BF16, OUT16, BM, BN, BK, WAVES_M, WAVES_N, NSTAGE, EPI_BIAS_GELU, SPLIT6>), dim3(grid), block, 0, s, a);
             break;
         case EPI_NONE:
-            hipLaunchKernelGGL((gemm_persistent_kernel<BF16, OUT16, BM, BN, BK, WAVES_M, WAVES_N, NSTAGE, EPI_NONE, BF16, SPLIT6>), dim3(grid), block, 0, s, a);
+            hipLaunchKernelGGL((gemm_persistent_kernel<BF16, OUT16, BM, BN, BK, WAVES_M, WAVES_N, NSTAGE, EPI_NONE, SPLIT6>), dim3(grid), block, 0, s, a);
             break;
         default:
             return hipErrorInvalidValue;
@@ -1303,8 +1303,7 @@ hipError_t launch_gemm_f32_add_ln(const GemmArgs& a, hipStream_t s) {
     if (tiles == 0) return hipSuccess;
     const int grid = std::min(tiles, cu_count());
     if (a.split6)
-        hipLaunchKernelGGL((gemm_persistent_kernel<false, false, ADD_LN_BM, ADD_LN_BN, ADD_LN_BK, 2, 4, 2, EPI_ADD_LN,
-                                                   false, true>),
+        hipLaunchKernelGGL((gemm_persistent_kernel<false, false, ADD_LN_BM, ADD_LN_BN, ADD_LN_BK, 2, 4, 2, EPI_ADD_LN, true>),
                            dim3(grid), dim3(512), 0, s, a);
     else
         hipLaunchKernelGGL((gemm_persistent_kernel<false, false, ADD_LN_BM, ADD_LN_BN, ADD_LN_BK, 2, 4, 2, EPI_ADD_LN>),
