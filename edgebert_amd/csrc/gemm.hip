@@ -20,6 +20,8 @@
 // summed are exactly those of the dot product.
 #include <algorithm>
 
+#include <type_traits>
+
 #include "kernels.hpp"
 
 namespace ebh {
@@ -739,120 +741,154 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_persistent_kernel
         else epilogue_tile(t, stage);
     };
 
-    point_at(0);
+    // k-slice s + 1's fragments are read while slice s's MFMAs run (two
+    // fragment sets in registers).  fp32 c3 forward 6.04 -> 6.00 ms against
+    // reading each slice's just before its MFMAs.
+    constexpr bool PREF = KS > 1;
+    v4f afb[PREF ? 2 : 1][FM], wfb[PREF ? 2 : 1][FN];
+    auto mfma_slice = [&](int b) __attribute__((always_inline)) {
+        const v4f (&af)[FM] = afb[b];
+        const v4f (&wf)[FN] = wfb[b];
+        if constexpr (BF16) {
 #pragma unroll
-    for (int d = 0; d < D; ++d)
-        if (nit < total) issue();
-    int it = 0;
-    for (int t = 0; t < my_tiles; ++t) {
-        for (int kt = 0; kt < nk; ++kt, ++it) {
-            // k-tile `it` has landed once only the loads issued after it remain.
-            int after = 0;
-            for (int j = it + 1; j < nit; ++j) after += n_issued(j);
-            wait_vmcnt(after);
-            lds_barrier();
-            if (kt == 0) {
-                if (!LN && t > 0) {
-                    finish_tile(t - 1, smem + ((it - 1) % NSTAGE) * STAGE);
-                    lds_barrier();  // the stage is refilled by the loads below
-                }
-#pragma unroll
-                for (int i = 0; i < FM; ++i)
-#pragma unroll
-                    for (int j = 0; j < FN; ++j)
-#pragma unroll
-                        for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
-            }
-            const bool refill = nit < total;
-            const float* st = smem + (it % NSTAGE) * STAGE;
-            // k-slice s + 1's fragments are read while slice s's MFMAs run
-            // (two fragment sets in registers).  fp32 c3 forward 6.04 ->
-            // 6.00 ms against reading each slice's just before its MFMAs.
-            constexpr bool PREF = KS > 1;
-            v4f afb[PREF ? 2 : 1][FM], wfb[PREF ? 2 : 1][FN];
-            auto rd = [&](int s, int b) __attribute__((always_inline)) {
-                const int ko = 4 * ((2 * s + half) ^ sw);
-#pragma unroll
-                for (int i = 0; i < FM; ++i)
-                    afb[b][i] = *reinterpret_cast<const v4f*>(st + a_row + i * 32 * RW + ko);
+            for (int i = 0; i < FM; ++i)
 #pragma unroll
                 for (int j = 0; j < FN; ++j)
-                    wfb[b][j] = *reinterpret_cast<const v4f*>(st + w_row + j * 32 * RW + ko);
-            };
-            if constexpr (SPLIT6) {
-                static_assert(!BF16 && KS % 2 == 0, "split products: fp32 tiles of whole 16-deep slices");
-                // fp32 A and W fragments, split in registers into bf16 parts
-                // h + m + l; six bf16 MFMAs per block and 16-deep slice (the
-                // smallest products first).  Lane half h takes k = 16 sp +
-                // 8 h .. +7: fp32 chunks 4 sp + 2 h and 4 sp + 2 h + 1.
+                    acc[i][j] = PACKED
+                        ? __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+                              __builtin_bit_cast(v8bf, wf[j]), __builtin_bit_cast(v8bf, af[i]), acc[i][j], 0, 0, 0)
+                        : __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+                              __builtin_bit_cast(v8bf, af[i]), __builtin_bit_cast(v8bf, wf[j]), acc[i][j], 0, 0, 0);
+        } else {
 #pragma unroll
-                for (int sp = 0; sp < KS / 2; ++sp) {
-                    if (refill && sp < NPART) issue_part(sp);
-                    const int c0 = 4 * sp + 2 * half;
-                    const int ko0 = 4 * (c0 ^ sw), ko1 = 4 * ((c0 + 1) ^ sw);
-                    v8bf wh[FN], wm[FN], wl[FN];
+            for (int q = 0; q < 4; ++q)
+#pragma unroll
+                for (int i = 0; i < FM; ++i)
 #pragma unroll
                     for (int j = 0; j < FN; ++j)
-                        split3_bf16(*reinterpret_cast<const v4f*>(st + w_row + j * 32 * RW + ko0),
-                                    *reinterpret_cast<const v4f*>(st + w_row + j * 32 * RW + ko1), wh[j], wm[j], wl[j]);
+                        acc[i][j] = PACKED
+                            ? __builtin_amdgcn_mfma_f32_32x32x2f32(wf[j][q], af[i][q], acc[i][j], 0, 0, 0)
+                            : __builtin_amdgcn_mfma_f32_32x32x2f32(af[i][q], wf[j][q], acc[i][j], 0, 0, 0);
+        }
+    };
+    // The MFMAs of each k-tile's last slice (fragments already in registers,
+    // set 1) wait until after the next k-tile's barrier and the issue of its
+    // first fragment reads, so the MFMA pipes keep working through the
+    // barrier and the latency of those reads.  At a tile's end they run
+    // before its epilogue (after the next tile's first barrier, so also
+    // there).  The first k-tile of a tile is peeled off, so that no MFMA sits
+    // behind a branch on the k-tile index: accumulators merged from two paths
+    // cost the register allocator a second copy of them.
+    constexpr bool DEFER = PREF && KS % 2 == 0 && !SPLIT6;
+    if constexpr (DEFER) {
 #pragma unroll
-                    for (int i = 0; i < FM; ++i) {
-                        v8bf ah, am, al;
-                        split3_bf16(*reinterpret_cast<const v4f*>(st + a_row + i * 32 * RW + ko0),
-                                    *reinterpret_cast<const v4f*>(st + a_row + i * 32 * RW + ko1), ah, am, al);
+        for (int i = 0; i < FM; ++i) afb[1][i] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-                        for (int j = 0; j < FN; ++j) {
-                            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(al, wh[j], acc[i][j], 0, 0, 0);
-                            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(am, wm[j], acc[i][j], 0, 0, 0);
-                            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah, wl[j], acc[i][j], 0, 0, 0);
-                            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(am, wh[j], acc[i][j], 0, 0, 0);
-                            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah, wm[j], acc[i][j], 0, 0, 0);
-                            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah, wh[j], acc[i][j], 0, 0, 0);
-                        }
+        for (int j = 0; j < FN; ++j) wfb[1][j] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+    }
+
+    int it = 0;
+    // Wait until k-tile `it` has landed in every wave's part: only the loads
+    // issued after it may remain outstanding.
+    auto enter_ktile = [&]() __attribute__((always_inline)) {
+        int after = 0;
+        for (int j = it + 1; j < nit; ++j) after += n_issued(j);
+        wait_vmcnt(after);
+        lds_barrier();
+    };
+    // The MFMAs of k-tile `it` (its loads have landed), and the loads of a
+    // later k-tile spread over its first slices.
+    auto run_ktile = [&](auto first) __attribute__((always_inline)) {
+        const bool refill = nit < total;
+        const float* st = smem + (it % NSTAGE) * STAGE;
+        auto rd = [&](int s, int b) __attribute__((always_inline)) {
+            const int ko = 4 * ((2 * s + half) ^ sw);
+#pragma unroll
+            for (int i = 0; i < FM; ++i)
+                afb[b][i] = *reinterpret_cast<const v4f*>(st + a_row + i * 32 * RW + ko);
+#pragma unroll
+            for (int j = 0; j < FN; ++j)
+                wfb[b][j] = *reinterpret_cast<const v4f*>(st + w_row + j * 32 * RW + ko);
+        };
+        if constexpr (SPLIT6) {
+            static_assert(!BF16 && KS % 2 == 0, "split products: fp32 tiles of whole 16-deep slices");
+            // fp32 A and W fragments, split in registers into bf16 parts
+            // h + m + l; six bf16 MFMAs per block and 16-deep slice (the
+            // smallest products first).  Lane half h takes k = 16 sp +
+            // 8 h .. +7: fp32 chunks 4 sp + 2 h and 4 sp + 2 h + 1.
+#pragma unroll
+            for (int sp = 0; sp < KS / 2; ++sp) {
+                if (refill && sp < NPART) issue_part(sp);
+                const int c0 = 4 * sp + 2 * half;
+                const int ko0 = 4 * (c0 ^ sw), ko1 = 4 * ((c0 + 1) ^ sw);
+                v8bf wh[FN], wm[FN], wl[FN];
+#pragma unroll
+                for (int j = 0; j < FN; ++j)
+                    split3_bf16(*reinterpret_cast<const v4f*>(st + w_row + j * 32 * RW + ko0),
+                                *reinterpret_cast<const v4f*>(st + w_row + j * 32 * RW + ko1), wh[j], wm[j], wl[j]);
+#pragma unroll
+                for (int i = 0; i < FM; ++i) {
+                    v8bf ah, am, al;
+                    split3_bf16(*reinterpret_cast<const v4f*>(st + a_row + i * 32 * RW + ko0),
+                                *reinterpret_cast<const v4f*>(st + a_row + i * 32 * RW + ko1), ah, am, al);
+#pragma unroll
+                    for (int j = 0; j < FN; ++j) {
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(al, wh[j], acc[i][j], 0, 0, 0);
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(am, wm[j], acc[i][j], 0, 0, 0);
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah, wl[j], acc[i][j], 0, 0, 0);
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(am, wh[j], acc[i][j], 0, 0, 0);
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah, wm[j], acc[i][j], 0, 0, 0);
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah, wh[j], acc[i][j], 0, 0, 0);
                     }
                 }
-                continue;
             }
+        } else {
             if (PREF) rd(0, 0);
+            if constexpr (DEFER && !decltype(first)::value) mfma_slice(1);   // k-tile it - 1's last slice
 #pragma unroll
             for (int s = 0; s < KS; ++s) {
                 if (refill && s < NPART) issue_part(s);
                 if (!PREF) rd(s, 0);
                 else if (s + 1 < KS) rd(s + 1, (s + 1) & 1);
-                const v4f (&af)[FM] = afb[PREF ? (s & 1) : 0];
-                const v4f (&wf)[FN] = wfb[PREF ? (s & 1) : 0];
-                if constexpr (BF16) {
-#pragma unroll
-                    for (int i = 0; i < FM; ++i)
-#pragma unroll
-                        for (int j = 0; j < FN; ++j)
-                            acc[i][j] = PACKED
-                                ? __builtin_amdgcn_mfma_f32_32x32x16_bf16(
-                                      __builtin_bit_cast(v8bf, wf[j]), __builtin_bit_cast(v8bf, af[i]), acc[i][j], 0, 0, 0)
-                                : __builtin_amdgcn_mfma_f32_32x32x16_bf16(
-                                      __builtin_bit_cast(v8bf, af[i]), __builtin_bit_cast(v8bf, wf[j]), acc[i][j], 0, 0, 0);
-                } else {
-#pragma unroll
-                    for (int q = 0; q < 4; ++q)
-#pragma unroll
-                        for (int i = 0; i < FM; ++i)
-#pragma unroll
-                            for (int j = 0; j < FN; ++j)
-                                acc[i][j] = PACKED
-                                    ? __builtin_amdgcn_mfma_f32_32x32x2f32(wf[j][q], af[i][q], acc[i][j], 0, 0, 0)
-                                    : __builtin_amdgcn_mfma_f32_32x32x2f32(af[i][q], wf[j][q], acc[i][j], 0, 0, 0);
-                }
+                if (!(DEFER && s == KS - 1)) mfma_slice(PREF ? (s & 1) : 0);
             }
+        }
+    };
+
+    point_at(0);
+#pragma unroll
+    for (int d = 0; d < D; ++d)
+        if (nit < total) issue();
+    for (int t = 0; t < my_tiles; ++t) {
+        enter_ktile();
+        if constexpr (DEFER && !LN) mfma_slice(1);   // the previous tile's last slice (zeros at t = 0)
+        if (!LN && t > 0) {
+            finish_tile(t - 1, smem + ((it - 1) % NSTAGE) * STAGE);
+            lds_barrier();  // the stage is refilled by the loads below
+        }
+#pragma unroll
+        for (int i = 0; i < FM; ++i)
+#pragma unroll
+            for (int j = 0; j < FN; ++j)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+        run_ktile(std::true_type{});
+        ++it;
+        for (int kt = 1; kt < nk; ++kt, ++it) {
+            enter_ktile();
+            run_ktile(std::false_type{});
         }
         // EPI_ADD_LN: one epilogue site, at the end of each tile (the next
         // tile's first k-tile is already on its way into the other stage).
         if constexpr (LN) {
+            if constexpr (DEFER) mfma_slice(1);
             lds_barrier();  // every wave is done with this tile's last stage
             finish_tile(t, smem + ((it - 1) % NSTAGE) * STAGE);
             lds_barrier();  // that stage is refilled next
         }
     }
     if constexpr (!LN) {
+        if constexpr (DEFER) mfma_slice(1);
         lds_barrier();  // every wave is done with the last k-tile's stage
         finish_tile(my_tiles - 1, smem + ((it - 1) % NSTAGE) * STAGE);
     }
