@@ -48,16 +48,31 @@ KERNELS = ("gemm_qkv", "attention", "gemm_out", "gemm_ffn_up", "gemm_ffn_down", 
            "embed", "pool")
 
 
-def kernel_work(cfg, lengths, B: int, which: str):
+def few_fused(cfg, B: int, S: int, dtype: str) -> bool:
+    """Whether the library runs attention and the attention-output projection
+    of this batch as one launch (the rule of few_attn_fits in
+    edgebert_amd/csrc/few.hip): fp32 GEMMs, at most 64 positions, hidden 384
+    in heads of 32.  Its profiled "attention" launch then includes the output
+    projection's partials."""
+    H, nh = cfg.hidden_size, cfg.num_attention_heads
+    return dtype != "bf16" and 0 < B * S <= 64 and H == 384 and H == 32 * nh
+
+
+def kernel_work(cfg, lengths, B: int, which: str, fused: bool = False):
     """Algorithmic work of ONE launch of a kernel family: (amount, bound, unit).
 
     GEMMs: 2*T*N*K FLOPs over the T valid tokens.  Attention: 4*H*sum(l^2)
     FLOPs (q.k^T and p.v at 2 FLOP per MAC).  Row kernels: the HBM bytes the
     op must move at minimum (each operand read once, each result written once).
+    fused: the few-token layer's launches (few_fused).
     """
     H, I = cfg.hidden_size, cfg.intermediate_size
     lengths = np.asarray(lengths, np.float64)
     T = float(lengths.sum())
+    if fused and which == "attention":
+        return 2.0 * T * H * H + 4.0 * H * float((lengths ** 2).sum()), "mfma", "flop"
+    if fused and which == "gemm_out":
+        raise KeyError("gemm_out runs inside the attention launch at this size")
     if which == "gemm_qkv":
         return 2.0 * T * H * 3 * H, "mfma", "flop"
     if which == "gemm_out":
@@ -233,15 +248,20 @@ def split_product_run(eb, torch, spec, weights, d_ids, d_mask, d_ref, lengths, s
     launches, prof_ms = m.profile_read()
     m.profile_enable("none")
     m.close()
-    work, bound, wunit = kernel_work(cfg, lengths, B, profile_kernel)
+    # At most 64 positions the few-token kernels run plain fp32 MFMA products
+    # for this dtype too (their products are memory round trips, not MFMA work).
+    few = B * S <= 64
+    work, bound, wunit = kernel_work(cfg, lengths, B, profile_kernel, few_fused(cfg, B, S, "fp32-bf16x6"))
     avg = prof_ms / max(launches, 1)
-    peak = PEAK_TFLOPS["fp32-bf16x6"] if bound == "mfma" else HBM_PEAK_GBS
+    peak = PEAK_TFLOPS["fp32" if few else "fp32-bf16x6"] if bound == "mfma" else HBM_PEAK_GBS
     achieved = work / (avg * 1e-3) / (1e12 if bound == "mfma" else 1e9)
     return {"value": round(B * steps / wall, 2), "unit": "sentences/s",
             "ms_per_step": round(1e3 * wall / steps, 4),
             "p50_batch_latency_ms": round(float(np.median(times)) * 1e3, 4),
             "max_abs_vs_fp32_path": max_abs,
-            "gemm_arithmetic": "fp32 operands split into three bf16 parts, six bf16 MFMA products "
+            "gemm_arithmetic": "fp32 MFMA products: at most 64 positions the few-token kernels do not "
+                               "split (EBH_DTYPE_F32_BF16X6)" if few else
+                               "fp32 operands split into three bf16 parts, six bf16 MFMA products "
                                "per fp32 product, fp32 accumulate (EBH_DTYPE_F32_BF16X6)",
             "roofline": {"kernel": profile_kernel, "bound": bound, "achieved": round(achieved, 3),
                          "peak": round(peak, 1), "unit": "TFLOP/s" if bound == "mfma" else "GB/s",
@@ -336,7 +356,8 @@ def main():
     value = B * args.steps / wall
     tokens = int(mask.sum())
     avg_kernel_ms = prof_ms / max(launches, 1)
-    work, bound, wunit = kernel_work(cfg, lengths, B, args.profile_kernel)
+    fused = few_fused(cfg, B, S, dtype)
+    work, bound, wunit = kernel_work(cfg, lengths, B, args.profile_kernel, fused)
     if bound == "mfma":
         achieved, peak, punit = work / (avg_kernel_ms * 1e-3) / 1e12, PEAK_TFLOPS[dtype], "TFLOP/s"
     else:
@@ -365,7 +386,9 @@ def main():
                    "parallelism": "single GPU"},
         "forward_tflops": round(fwd_flops / (ms_per_step * 1e-3) / 1e12, 2),
         "graph_replay": not args.no_graph_replay,
-        "roofline": {"kernel": args.profile_kernel, "bound": bound, "achieved": round(achieved, 3),
+        "roofline": {"kernel": args.profile_kernel + (" (with the output projection)"
+                                                      if fused and args.profile_kernel == "attention" else ""),
+                     "bound": bound, "achieved": round(achieved, 3),
                      "peak": peak, "unit": punit, "frac": round(achieved / peak, 4),
                      "traffic": measured_traffic(args.config, args.profile_kernel, dtype),
                      "work_per_launch": work, "work_unit": wunit,

@@ -260,9 +260,12 @@ size_t layout_workspace(const ebh_model* m, int64_t tcap, int bcap, char* base, 
     const ebh_config& c = m->cfg;
     const size_t H = c.hidden_size, I = c.intermediate_size;
     const bool b16 = m->dtype == EBH_DTYPE_BF16;
-    const int yparts = b16 ? 1
-                           : std::max(ebh::gemm_f32_splits((int)tcap, (int)H, (int)H),
-                                      ebh::gemm_f32_splits((int)tcap, (int)H, (int)I));
+    int yparts = b16 ? 1
+                     : std::max(ebh::gemm_f32_splits((int)tcap, (int)H, (int)H),
+                                ebh::gemm_f32_splits((int)tcap, (int)H, (int)I));
+    // Few-token attention + output projection: one partial per head.
+    if (!b16 && ebh::few_attn_fits((int)tcap, (int)H, c.num_attention_heads))
+        yparts = std::max(yparts, c.num_attention_heads);
     size_t off = 0;
     auto take = [&](size_t bytes) { size_t o = off; off += align_up(std::max<size_t>(bytes, 1)); return o; };
     const size_t oErr = take(4), oX = take(b16 ? 0 : tcap * H * 4), oX16 = take(b16 ? tcap * H * 2 : 0),
@@ -457,6 +460,9 @@ int enqueue_kernels(ebh_model* m, Workspace& w, const int* d_ids, const int* d_m
         return sp;
     };
     const int sp_out = splits_for(H), sp_down = splits_for(I);
+    // At most FEW_ATTN_MAX_TOKENS rows (fp32, heads of 32): attention and the
+    // output projection run as one launch writing a partial per head.
+    const bool few_attn = !bf16 && ebh::few_attn_fits(T, H, nh) && T_od == T && part_cap >= nh;
     auto gemm_ln = [&](int kind, const float* A, const float* W, const float* bias, const float* g,
                        const float* b, int K) -> int {
         ebh::GemmArgs a{};
@@ -491,12 +497,19 @@ int enqueue_kernels(ebh_model* m, Workspace& w, const int* d_ids, const int* d_m
                        bf16 ? (void*)qkv16 : (void*)w.QKV, 3 * H, H, ebh::EPI_BIAS, bf16)))
             return rc;
         prof_begin(m, prof_kind, EBH_PROF_ATTENTION, s, pp, on);
-        if (bf16)
+        if (few_attn)
+            HIP_TRY(ebh::launch_attn_out_few(w.QKV, L.wo, w.cu, w.ntok, B, T, H, nh, scale, w.Y, (int64_t)T * H,
+                                             s));
+        else if (bf16)
             HIP_TRY(ebh::launch_attention_bf16(qkv16, w.cu, B, S, H, nh, hd, scale, ctx16, s));
         else
             HIP_TRY(ebh::launch_attention(w.QKV, w.cu, B, S, H, nh, hd, scale, w.CTX, s));
         prof_end(m, s, pp, on);
-        if (fuse_out) {
+        if (few_attn) {
+            prof_begin(m, prof_kind, EBH_PROF_LAYERNORM, s, pp, on);
+            HIP_TRY(add_ln(L.bo, L.ln1_g, L.ln1_b, nh));
+            prof_end(m, s, pp, on);
+        } else if (fuse_out) {
             if ((rc = gemm_ln(EBH_PROF_GEMM_OUT, w.CTX, L.wo, L.bo, L.ln1_g, L.ln1_b, H))) return rc;
         } else {
             if ((rc = gemm(EBH_PROF_GEMM_OUT, bf16 ? (const void*)ctx16 : w.CTX, H, L.wo, L.wo16, nullptr,

@@ -224,35 +224,8 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_f32_kernel(GemmAr
 // row-contiguous float4.  Its stores are then older than every load still to
 // be waited for, so no later wait depends on them finishing early.
 // ---------------------------------------------------------------------------
-// tanh-form GELU of the reference (constants of src/lib.rs:151-152),
-// 0.5 x (1 + tanh(u)) with u = sqrt(2/pi) (x + 0.044715 x^3), evaluated as
-// x * sigmoid(2u) = x / (1 + e^(-2u)) on the hardware exp2 and reciprocal:
-// five VALU operations besides those two, and no cancellation for negative x
-// (e^(-2u) = inf gives -0 for finite x; x = +inf gives +inf, -inf gives NaN,
-// as the tanh form does).
-//
-// Error bound (eps = 2^-24, t = x (K1 + K2 x^2) the exponent passed to exp2),
-// against the same formula in exact arithmetic with the reference's decimal
-// constants: K1 and K2 are rounded products of rounded constants (3 and 5
-// eps); s = fma(x^2, K2, K1) adds the rounding of x^2 and its own (its two
-// terms have the same sign, so nothing cancels): 7 eps; t = x s: 8 eps.
-// exp2 turns a relative error d of t into |t| d ln 2 of e, plus its own
-// 1 ulp; 1 + e, the reciprocal and the final product add 4 eps, and e's
-// error reaches the result scaled by e / (1 + e) <= 1.  So
-//   |gelu_fast(x) - gelu(x)| <= (8 ln2 |t| + 8) eps |gelu(x)|,
-// e.g. <= 8.5e-6 relative for x >= -5 (|t| <= 25), <= 6e-7 for x >= 0.
-// Where t > 126 (x < -9.7) e leaves the fp32 range and the result is -0 or a
-// value below 2^-126, against a true value below 1e-36.
-// ebh_op_gelu (test_gpu_ops.py) checks this bound over [-12, 12] against the
-// float64 tanh form.
-__device__ __forceinline__ float gelu_tanh_fast(float val) {
-    // -2 * log2(e) * sqrt(2/pi), and that times 0.044715
-    const float K1 = -2.0f * 1.4426950408889634f * 0.7978845608f;
-    const float K2 = K1 * 0.044715f;
-    const float e = __builtin_amdgcn_exp2f(val * fmaf(val * val, K2, K1));  // e^(-2u)
-    return val * __builtin_amdgcn_rcpf(1.0f + e);
-}
 
+// Standalone GELU (ebh_op_gelu): gelu_tanh_fast over n floats.
 __global__ __launch_bounds__(256) void gelu_kernel(const float* __restrict__ x, float* __restrict__ y, int64_t n) {
     for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256)
         y[i] = gelu_tanh_fast(x[i]);

@@ -117,6 +117,19 @@ hipError_t launch_pack_embed_few(const int* ids, const int* mask, int B, int S, 
                                  const float* type0, const float* g, const float* b, int V, int H, float eps,
                                  float* x, uint16_t* x16, hipStream_t s);
 
+// Attention + the attention-output projection at a handful of tokens (fp32,
+// few.hip): at most FEW_ATTN_MAX_TOKENS rows (T_max, the rows the workspace is
+// sized for; the packed count is read from ntok), H = 384 in heads of 32.
+// Takes the QKV projection (with its bias, [T, 3H]) and writes nh partial
+// attention-output products (each head's context times its 32 columns of Wo;
+// no bias) at Y + h * part_stride; launch_add_layernorm with nh parts
+// finishes the block.
+constexpr int FEW_ATTN_MAX_TOKENS = 64;
+bool few_attn_fits(int T_max, int H, int nh);
+hipError_t launch_attn_out_few(const float* qkv, const float* wo, const int* cu, const int* ntok, int B,
+                              int T_max, int H, int nh, float scale, float* Y, int64_t part_stride,
+                              hipStream_t s);
+
 // Embedding gather + position + token type 0 + LayerNorm over packed tokens,
 // into x (fp32) and / or x16 (bf16; either may be nullptr, not both).
 hipError_t launch_embed_ln(const int* tok_id, const int* tok_pos, const int* n_tokens,
@@ -181,6 +194,35 @@ __device__ __forceinline__ float gelu_tanh(float val) {
     float val_cubed = val * val * val;
     float inner = SQRT_2_OVER_PI * (val + GELU_COEFF * val_cubed);
     return val * 0.5f * (1.0f + tanhf(inner));
+}
+
+// tanh-form GELU of the reference (constants of src/lib.rs:151-152),
+// 0.5 x (1 + tanh(u)) with u = sqrt(2/pi) (x + 0.044715 x^3), evaluated as
+// x * sigmoid(2u) = x / (1 + e^(-2u)) on the hardware exp2 and reciprocal:
+// five VALU operations besides those two, and no cancellation for negative x
+// (e^(-2u) = inf gives -0 for finite x; x = +inf gives +inf, -inf gives NaN,
+// as the tanh form does).
+//
+// Error bound (eps = 2^-24, t = x (K1 + K2 x^2) the exponent passed to exp2),
+// against the same formula in exact arithmetic with the reference's decimal
+// constants: K1 and K2 are rounded products of rounded constants (3 and 5
+// eps); s = fma(x^2, K2, K1) adds the rounding of x^2 and its own (its two
+// terms have the same sign, so nothing cancels): 7 eps; t = x s: 8 eps.
+// exp2 turns a relative error d of t into |t| d ln 2 of e, plus its own
+// 1 ulp; 1 + e, the reciprocal and the final product add 4 eps, and e's
+// error reaches the result scaled by e / (1 + e) <= 1.  So
+//   |gelu_fast(x) - gelu(x)| <= (8 ln2 |t| + 8) eps |gelu(x)|,
+// e.g. <= 8.5e-6 relative for x >= -5 (|t| <= 25), <= 6e-7 for x >= 0.
+// Where t > 126 (x < -9.7) e leaves the fp32 range and the result is -0 or a
+// value below 2^-126, against a true value below 1e-36.
+// ebh_op_gelu (test_gpu_ops.py) checks this bound over [-12, 12] against the
+// float64 tanh form.
+__device__ __forceinline__ float gelu_tanh_fast(float val) {
+    // -2 * log2(e) * sqrt(2/pi), and that times 0.044715
+    const float K1 = -2.0f * 1.4426950408889634f * 0.7978845608f;
+    const float K2 = K1 * 0.044715f;
+    const float e = __builtin_amdgcn_exp2f(val * fmaf(val * val, K2, K1));  // e^(-2u)
+    return val * __builtin_amdgcn_rcpf(1.0f + e);
 }
 
 // One lane's 16 bytes from global memory straight into LDS

@@ -4,7 +4,7 @@ own resource-usage remarks (hipcc -Rpass-analysis=kernel-resource-usage).
     python3 edgebert_amd/csrc/resource_report.py [--fail-on-scratch]
 
 prints one line per kernel (VGPRs, AGPRs, scratch bytes per lane, SGPR / VGPR
-spills, occupancy) for gemm.hip, attention.hip and rowops.hip, and with
+spills, occupancy) for gemm.hip, attention.hip, rowops.hip and few.hip, and with
 --fail-on-scratch exits 1 if any kernel spills or uses scratch."""
 import os
 import re
@@ -42,7 +42,7 @@ def demangle(names):
 
 def main():
     bad = 0
-    for src in ("gemm.hip", "attention.hip", "rowops.hip"):
+    for src in ("gemm.hip", "attention.hip", "rowops.hip", "few.hip"):
         rows = kernels(src)
         names = demangle([r["name"] for r in rows])
         print(f"{src}: {len(rows)} kernels")

@@ -285,13 +285,13 @@ __device__ __forceinline__ void ln_row4(float4 (&v)[NV], int sub, int H, const f
 // order, with their loads going out PB partials at a time (an index past the
 // last partial re-reads the last one and is not added), so a row waits for
 // one memory round trip per PB partials rather than one per partial.
-template <int NV, int LPR, int PB>
+template <int NV, int LPR, int PB, int BS = 256>
 __device__ __forceinline__ void add_layernorm4_row(const float* __restrict__ y, const float* __restrict__ bias,
                                                    float* x, const float* __restrict__ g,
                                                    const float* __restrict__ bta, int rows_max,
                                                    const int* rows_dev, int H, float eps, uint16_t* x16,
                                                    int nparts, int64_t part_stride) {
-    constexpr int RPB = 256 / LPR;                // rows per workgroup
+    constexpr int RPB = BS / LPR;                 // rows per workgroup
     const int row = blockIdx.x * RPB + threadIdx.x / LPR, sub = threadIdx.x % LPR;
     const int rows = rows_dev ? *rows_dev : rows_max;
     if (row >= rows) return;
@@ -344,6 +344,19 @@ __device__ __forceinline__ void add_layernorm4_row(const float* __restrict__ y, 
     }
 EBH_ADD_LN4_KERNEL(add_layernorm4_kernel, 0)       // one product
 EBH_ADD_LN4_KERNEL(add_layernorm4_p4_kernel, 4)    // split-K partials
+// More than 8 partials at a handful of rows (the few-token attention's one
+// per head): one row per workgroup (LPR threads), the partials read 16 at a
+// time (4 where the row takes more than 3 float4 per lane, for registers).  A
+// compute unit streams only about 10 bytes per clock from beyond its cache,
+// so the rows' partials are spread over as many of them as there are rows.
+template <int NV, int LPR>
+__global__ __launch_bounds__(LPR) void add_layernorm4_row1_kernel(
+    const float* __restrict__ y, const float* __restrict__ bias, float* x, const float* __restrict__ g,
+    const float* __restrict__ bta, int rows_max, const int* rows_dev, int H, float eps, uint16_t* x16, int nparts,
+    int64_t part_stride) {
+    add_layernorm4_row<NV, LPR, (NV <= 3 ? 16 : 4), LPR>(y, bias, x, g, bta, rows_max, rows_dev, H, eps, x16,
+                                                           nparts, part_stride);
+}
 #undef EBH_ADD_LN4_KERNEL
 
 // The same with the projection y stored as bf16 (bf16 models write the
@@ -603,6 +616,24 @@ hipError_t launch_add_layernorm(const float* y, const float* bias, float* x, con
     row4_shape(H, lpr, nv);
     if (lpr && al16(y) && al16(bias) && al16(x) && al16(g) && al16(b) && (!x16 || ((uintptr_t)x16 & 7) == 0) &&
         part_stride % 4 == 0) {
+        // Partials are read PB at a time, each group one memory round trip.
+        if (nparts > 8 && rows_max <= 64) {
+#define EBH_LN_ROW1(L)                                                                                  \
+            if (lpr == L) {                                                                         \
+                switch (nv) {                                                                       \
+                    case 1: hipLaunchKernelGGL((add_layernorm4_row1_kernel<1, L>), dim3(rows_max), dim3(L), 0, s, \
+                                               y, bias, x, g, b, rows_max, rows_dev, H, eps, x16, nparts, part_stride); break; \
+                    case 2: hipLaunchKernelGGL((add_layernorm4_row1_kernel<2, L>), dim3(rows_max), dim3(L), 0, s, \
+                                               y, bias, x, g, b, rows_max, rows_dev, H, eps, x16, nparts, part_stride); break; \
+                    case 3: hipLaunchKernelGGL((add_layernorm4_row1_kernel<3, L>), dim3(rows_max), dim3(L), 0, s, \
+                                               y, bias, x, g, b, rows_max, rows_dev, H, eps, x16, nparts, part_stride); break; \
+                    default: return hipErrorInvalidValue;                                           \
+                }                                                                                   \
+                return hipGetLastError();                                                           \
+            }
+            EBH_LN_ROW1(64) EBH_LN_ROW1(32) EBH_LN_ROW1(16)
+#undef EBH_LN_ROW1
+        }
         if (nparts > 1)
             EBH_ROW4_DISPATCH(add_layernorm4_p4_kernel, lpr, nv, rows_max, s, y, bias, x, g, b, rows_max,
                               rows_dev, H, eps, x16, nparts, part_stride);

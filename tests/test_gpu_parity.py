@@ -192,13 +192,17 @@ def test_c5_full_batch_bf16(eb, oracle_mod, weights_for):
 
 @pytest.mark.parametrize("model_name,B,S,lo,hi", [
     ("minilm", 1, 1, 1, 1), ("minilm", 5, 12, 3, 12), ("minilm", 4, 16, 16, 16),
-    ("minilm", 8, 8, 2, 8), ("bert", 2, 24, 9, 24)])
+    ("minilm", 8, 8, 2, 8), ("minilm", 2, 8, 8, 8), ("minilm", 64, 1, 1, 1), ("minilm", 3, 21, 1, 21),
+    ("bert", 2, 24, 9, 24)])
 def test_few_token_forwards(eb, oracle_mod, weights_for, model_name, B, S, lo, hi):
     """At most 64 padded tokens: every projection takes the few-token GEMM
     kernel (16-row blocks, the bias-free ones split over K), over 1 to 4 row
-    blocks with ragged last blocks.  Repeated calls (the later ones replayed
-    as a HIP graph) give bit-identical vectors; each sequence matches the
-    oracle's unpadded run."""
+    blocks with ragged last blocks; for MiniLM (heads of 32) attention and the
+    output projection run as one launch writing a partial per head, summed by
+    the one-row-per-workgroup LayerNorm (64 sequences of one token, a
+    sequence of 21 beside ones of a single token).  Repeated calls (the later
+    ones replayed as a HIP graph) give bit-identical vectors; each sequence
+    matches the oracle's unpadded run."""
     from edgebert_amd.synth import InputSpec, MINILM_L6, BERT_BASE, make_inputs
     cfg = MINILM_L6 if model_name == "minilm" else BERT_BASE
     spec = InputSpec(f"few_{model_name}_{B}x{S}", cfg, B, S, lo, hi, 20 + B * S)

@@ -1,6 +1,6 @@
 """No gfx950 kernel of the library spills registers or uses scratch memory:
-the compiler's resource-usage remarks for gemm.hip, attention.hip and
-rowops.hip (edgebert_amd/csrc/resource_report.py).  CPU only (hipcc
+the compiler's resource-usage remarks for gemm.hip, attention.hip,
+rowops.hip and few.hip (edgebert_amd/csrc/resource_report.py).  CPU only (hipcc
 cross-compiles); skipped where hipcc is absent."""
 import os
 import subprocess
