@@ -32,6 +32,89 @@ namespace ebh {
 typedef float v16f __attribute__((ext_vector_type(16)));
 typedef float v4f __attribute__((ext_vector_type(4)));
 
+// One 128-key chunk of the fp32 kernel below for the wave's 32 queries:
+// S^T = K . Q^T, the key-padding mask, the online-softmax update and
+// context^T += V^T . P^T.  lim = real keys in the chunk (1..128); c2 = scale
+// log2(e).  Fewer VALU instructions matter here: on this chip the VALU does
+// not issue while an fp32 MFMA of the same SIMD runs, so the softmax's
+// instructions add to the MFMA time instead of hiding behind it.
+template <int HD>
+__device__ __forceinline__ void attend_chunk(const float* Ks, const float* Vs, const v4f* qf, float c2, int l32,
+                                             int half, int lim, v16f* o, float& m_run, float& l_run, bool first) {
+    constexpr int KS = HD + 4, NJ = HD / 32;
+    v16f sc[4];
+    float cmax = -INFINITY;
+    const int lim_h = lim - 4 * half;   // key kb*32 + 8(r/4) + r%4 + 4 half is real iff kb*32 + 8(r/4) + r%4 < lim_h
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb) {
+        if (kb * 32 < lim) {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) sc[kb][r] = 0.0f;
+            const float* kr = Ks + (kb * 32 + l32) * KS + 4 * half;
+#pragma unroll
+            for (int s = 0; s < HD / 8; ++s) {
+                const v4f kf = *reinterpret_cast<const v4f*>(kr + s * 8);
+#pragma unroll
+                for (int q = 0; q < 4; ++q) sc[kb] = __builtin_amdgcn_mfma_f32_32x32x2f32(kf[q], qf[s][q], sc[kb], 0, 0, 0);
+            }
+            // Key-padding mask (src/lib.rs:887-891), only in the block that
+            // straddles the sequence end; the row max is taken over the raw
+            // scores (scale > 0 commutes with max).
+            if ((kb + 1) * 32 > lim) {
+#pragma unroll
+                for (int r = 0; r < 16; ++r)
+                    if (kb * 32 + 8 * (r >> 2) + (r & 3) >= lim_h) sc[kb][r] = -INFINITY;
+            }
+#pragma unroll
+            for (int r = 0; r < 16; ++r) cmax = fmaxf(cmax, sc[kb][r]);
+        }
+    }
+    cmax = fmaxf(cmax, __shfl_xor(cmax, 32));
+    // exp(scale (s - m)) as 2^(s c - m c), c = scale log2(e): the scale after
+    // q.k^T (src/lib.rs:714) folded into one FMA per score.  m and m_run are
+    // raw-score maxima; alpha = 0 on the first chunk.  The exponent is off by
+    // at most 3 eps |s c - m c| + eps |m c| (the roundings of c, m c and the
+    // FMA; eps = 2^-24), which exp2 turns into a relative error of that times
+    // ln 2 plus its own 1 ulp.
+    const float m_new = fmaxf(m_run, cmax);
+    const float mc = m_new * c2;
+    const float alpha = __builtin_amdgcn_exp2f(m_run * c2 - mc);
+    float ps[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb) {
+        if (kb * 32 < lim) {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const float pr = __builtin_amdgcn_exp2f(fmaf(sc[kb][r], c2, -mc));
+                sc[kb][r] = pr;
+                ps[r & 3] += pr;
+            }
+        }
+    }
+    l_run = l_run * alpha + ((ps[0] + ps[1]) + (ps[2] + ps[3]));
+    m_run = m_new;
+    if (!first) {
+#pragma unroll
+        for (int j = 0; j < NJ; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) o[j][r] *= alpha;
+    }
+    // context^T += V^T . P^T: A = V^T (row = dim l32, one key per lane half),
+    // B = P^T (that key, column = query l32).
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb) {
+        if (kb * 32 < lim) {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int key = kb * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
+#pragma unroll
+                for (int j = 0; j < NJ; ++j)
+                    o[j] = __builtin_amdgcn_mfma_f32_32x32x2f32(Vs[key * HD + j * 32 + l32], sc[kb][r], o[j], 0, 0, 0);
+            }
+        }
+    }
+}
+
 template <int HD>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(HD == 32 ? 3 : 2))) void attention_kernel(const float* __restrict__ qkv,
                                                         const int* __restrict__ cu_seqlens,
@@ -69,6 +152,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(HD == 32 ? 
 #pragma unroll
         for (int r = 0; r < 16; ++r) o[j][r] = 0.0f;
     float m_run = -INFINITY, l_run = 0.0f;
+    const float c_exp = scale * 1.4426950408889634f;   // exponent scale of the softmax (base 2)
 
     const int nchunks = (len + KC - 1) / KC;
     for (int c = 0; c < nchunks; ++c) {
@@ -102,70 +186,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(HD == 32 ? 
         }
         __syncthreads();
 
-        const int nkb = min(4, (len - kbase + 31) / 32);  // 32-key blocks holding real keys
-        v16f sc[4];
-        float cmax = -INFINITY;
-#pragma unroll
-        for (int kb = 0; kb < 4; ++kb) {
-            if (kb < nkb) {
-#pragma unroll
-                for (int r = 0; r < 16; ++r) sc[kb][r] = 0.0f;
-                const float* kr = Ks + (kb * 32 + l32) * KS + 4 * half;
-#pragma unroll
-                for (int s = 0; s < HD / 8; ++s) {
-                    const v4f kf = *reinterpret_cast<const v4f*>(kr + s * 8);
-#pragma unroll
-                    for (int q = 0; q < 4; ++q)
-                        sc[kb] = __builtin_amdgcn_mfma_f32_32x32x2f32(kf[q], qf[s][q], sc[kb], 0, 0, 0);
-                }
-#pragma unroll
-                for (int r = 0; r < 16; ++r) {
-                    const int key = kbase + kb * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
-                    float t = sc[kb][r] * scale;         // scale after q.k^T (src/lib.rs:714)
-                    if (key >= len) t = -INFINITY;       // key-padding mask (src/lib.rs:887-891)
-                    sc[kb][r] = t;
-                    cmax = fmaxf(cmax, t);
-                }
-            }
-        }
-        cmax = fmaxf(cmax, __shfl_xor(cmax, 32));
-        const float m_new = fmaxf(m_run, cmax);
-        const float alpha = fast_exp(m_run - m_new);  // 0 on the first chunk
-        float psum = 0.0f;
-#pragma unroll
-        for (int kb = 0; kb < 4; ++kb) {
-            if (kb < nkb) {
-#pragma unroll
-                for (int r = 0; r < 16; ++r) {
-                    const float pr = fast_exp(sc[kb][r] - m_new);
-                    sc[kb][r] = pr;
-                    psum += pr;
-                }
-            }
-        }
-        l_run = l_run * alpha + psum;
-        m_run = m_new;
-        if (c > 0) {
-#pragma unroll
-            for (int j = 0; j < NJ; ++j)
-#pragma unroll
-                for (int r = 0; r < 16; ++r) o[j][r] *= alpha;
-        }
-        // context^T += V^T . P^T over this chunk: A = V^T (row = dim l32, one
-        // key per lane half), B = P^T (that key, column = query l32).
-#pragma unroll
-        for (int kb = 0; kb < 4; ++kb) {
-            if (kb < nkb) {
-#pragma unroll
-                for (int r = 0; r < 16; ++r) {
-                    const int key = kb * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
-#pragma unroll
-                    for (int j = 0; j < NJ; ++j)
-                        o[j] = __builtin_amdgcn_mfma_f32_32x32x2f32(
-                            Vs[key * HD + j * 32 + l32], sc[kb][r], o[j], 0, 0, 0);
-                }
-            }
-        }
+        attend_chunk<HD>(Ks, Vs, qf, c_exp, l32, half, min(len - kbase, KC), o, m_run, l_run, c == 0);
     }
 
     // Normalise by the row sum (both lane halves hold partial sums) and store:
