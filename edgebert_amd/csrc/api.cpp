@@ -88,6 +88,7 @@ struct Workspace {
     float *X, *Y, *QKV, *CTX, *F;
     uint16_t* X16;  // bf16 copy of X (bf16 models: the GEMM input)
     int *ids, *mask, *counts, *cu, *ntok, *tok_id, *tok_pos, *err;
+    int* order;     // [B] sequences by decreasing length (written by launch_pack)
     float* out;
     float* scores;  // [B] cross-encoder scores
 };
@@ -271,7 +272,7 @@ size_t layout_workspace(const ebh_model* m, int64_t tcap, int bcap, char* base, 
     const size_t oErr = take(4), oX = take(b16 ? 0 : tcap * H * 4), oX16 = take(b16 ? tcap * H * 2 : 0),
                  oY = take((size_t)yparts * tcap * H * 4), oQKV = take(tcap * 3 * H * 4),
                  oCTX = take(tcap * H * 4), oF = take(tcap * I * 4), oIds = take(tcap * 4),
-                 oMask = take(tcap * 4), oCounts = take(bcap * 4), oCu = take((bcap + 1) * 4),
+                 oMask = take(tcap * 4), oCounts = take(bcap * 4), oOrder = take(bcap * 4), oCu = take((bcap + 1) * 4),
                  oNtok = take(4), oTid = take(tcap * 4), oTpos = take(tcap * 4),
                  oOut = take((size_t)bcap * H * 4), oScores = take((size_t)bcap * 4);
     if (!base) return off;
@@ -289,6 +290,7 @@ size_t layout_workspace(const ebh_model* m, int64_t tcap, int bcap, char* base, 
     w.ids = (int*)(base + oIds);
     w.mask = (int*)(base + oMask);
     w.counts = (int*)(base + oCounts);
+    w.order = (int*)(base + oOrder);
     w.cu = (int*)(base + oCu);
     w.ntok = (int*)(base + oNtok);
     w.tok_id = (int*)(base + oTid);
@@ -374,14 +376,16 @@ int enqueue_kernels(ebh_model* m, Workspace& w, const int* d_ids, const int* d_m
     ProfPair pp{};
     bool on = false;
     const bool bf16 = m->dtype == EBH_DTYPE_BF16;
-    if (ebh::pack_embed_few_fits(B, S, H)) {   // a few short sentences: one launch
+    const bool few_pack = ebh::pack_embed_few_fits(B, S, H);
+    const int* seq_order = few_pack ? nullptr : w.order;   // written by launch_pack only
+    if (few_pack) {   // a few short sentences: one launch
         prof_begin(m, prof_kind, EBH_PROF_EMBED, s, pp, on);
         HIP_TRY(ebh::launch_pack_embed_few(d_ids, d_mask, B, S, w.cu, w.ntok, w.tok_id, w.tok_pos, w.err,
                                            m->word, m->pos, m->type0, m->emb_g, m->emb_b, c.vocab_size, H,
                                            eps, bf16 ? nullptr : w.X, w.X16, s));
         prof_end(m, s, pp, on);
     } else {
-        HIP_TRY(ebh::launch_pack(d_ids, d_mask, B, S, w.counts, w.cu, w.ntok, w.tok_id, w.tok_pos, s));
+        HIP_TRY(ebh::launch_pack(d_ids, d_mask, B, S, w.counts, w.cu, w.ntok, w.tok_id, w.tok_pos, s, w.order));
         prof_begin(m, prof_kind, EBH_PROF_EMBED, s, pp, on);
         HIP_TRY(ebh::launch_embed_ln(w.tok_id, w.tok_pos, w.ntok, T, m->word, m->pos, m->type0,
                                      m->emb_g, m->emb_b, c.vocab_size, H, eps, bf16 ? nullptr : w.X, w.err,
@@ -501,9 +505,9 @@ int enqueue_kernels(ebh_model* m, Workspace& w, const int* d_ids, const int* d_m
             HIP_TRY(ebh::launch_attn_out_few(w.QKV, L.wo, w.cu, w.ntok, B, T, H, nh, scale, w.Y, (int64_t)T * H,
                                              s));
         else if (bf16)
-            HIP_TRY(ebh::launch_attention_bf16(qkv16, w.cu, B, S, H, nh, hd, scale, ctx16, s));
+            HIP_TRY(ebh::launch_attention_bf16(qkv16, w.cu, B, S, H, nh, hd, scale, ctx16, s, seq_order));
         else
-            HIP_TRY(ebh::launch_attention(w.QKV, w.cu, B, S, H, nh, hd, scale, w.CTX, s));
+            HIP_TRY(ebh::launch_attention(w.QKV, w.cu, B, S, H, nh, hd, scale, w.CTX, s, seq_order));
         prof_end(m, s, pp, on);
         if (few_attn) {
             prof_begin(m, prof_kind, EBH_PROF_LAYERNORM, s, pp, on);

@@ -119,14 +119,14 @@ template <int HD>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(HD == 32 ? 3 : 2))) void attention_kernel(const float* __restrict__ qkv,
                                                         const int* __restrict__ cu_seqlens,
                                                         float* __restrict__ ctx_out, int H,
-                                                        float scale) {
+                                                        float scale, const int* __restrict__ order) {
     constexpr int KC = 128;        // keys per LDS chunk
     constexpr int KS = HD + 4;     // K row stride (floats): conflict-free 16-B reads
     constexpr int NJ = HD / 32;    // 32-wide output blocks of the context
     __shared__ __attribute__((aligned(16))) float Ks[KC * KS];
     __shared__ __attribute__((aligned(16))) float Vs[KC * HD];
 
-    const int head = blockIdx.x, qb = blockIdx.y, b = blockIdx.z;
+    const int head = blockIdx.x, qb = blockIdx.y, b = order ? order[blockIdx.z] : (int)blockIdx.z;
     const int start = cu_seqlens[b];
     const int len = cu_seqlens[b + 1] - start;
     if (qb * 128 >= len) return;  // uniform over the workgroup
@@ -231,7 +231,7 @@ template <int HD>
 __global__ __launch_bounds__(256) void attention_bf16_kernel(const uint16_t* __restrict__ qkv,
                                                              const int* __restrict__ cu_seqlens,
                                                              uint16_t* __restrict__ ctx, int H,
-                                                             float scale) {
+                                                             float scale, const int* __restrict__ order) {
     constexpr int KC = 128;                 // keys per LDS chunk
     constexpr int KRS = HD + 8;             // K row stride (bf16): 16-byte padding, conflict-free b128 reads
     constexpr int VTS = KC + 8;             // Vt row stride (bf16): one row per head dim
@@ -240,7 +240,7 @@ __global__ __launch_bounds__(256) void attention_bf16_kernel(const uint16_t* __r
     __shared__ __attribute__((aligned(16))) uint16_t Ks[KC * KRS];
     __shared__ __attribute__((aligned(16))) uint16_t Vt[HD * VTS];
 
-    const int head = blockIdx.x, qb = blockIdx.y, b = blockIdx.z;
+    const int head = blockIdx.x, qb = blockIdx.y, b = order ? order[blockIdx.z] : (int)blockIdx.z;
     const int start = cu_seqlens[b];
     const int len = cu_seqlens[b + 1] - start;
     if (qb * 128 >= len) return;  // uniform over the workgroup
@@ -438,7 +438,7 @@ __device__ __forceinline__ int v_swizzle(int r) {
 template <int HD>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) void attention_bf16_short_kernel(
     const uint16_t* __restrict__ qkv, const int* __restrict__ cu_seqlens, uint16_t* __restrict__ ctx, int H,
-    float scale) {
+    float scale, const int* __restrict__ order) {
     constexpr int KC = 128;                 // keys (and queries) per sequence at most
     constexpr int CPR = HD / 8;             // 16-byte chunks per K / V row
     constexpr int TILE = KC * HD;           // bf16 elements of the K or V tile
@@ -448,7 +448,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
     __shared__ __attribute__((aligned(16))) uint16_t Ks[TILE];
     __shared__ __attribute__((aligned(16))) uint16_t Vs[TILE];
 
-    const int head = blockIdx.x, b = blockIdx.y;
+    const int head = blockIdx.x, b = order ? order[blockIdx.y] : (int)blockIdx.y;
     const int start = cu_seqlens[b];
     const int len = cu_seqlens[b + 1] - start;
     if (len == 0) return;  // uniform over the workgroup
@@ -587,38 +587,38 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
 
 hipError_t launch_attention_bf16(const uint16_t* qkv, const int* cu_seqlens, int B, int max_len,
                                  int H, int nh, int head_dim, float scale, uint16_t* ctx,
-                                 hipStream_t s) {
+                                 hipStream_t s, const int* order) {
     if (B <= 0 || max_len <= 0) return hipSuccess;
     if (max_len <= 128) {
         // One key chunk per sequence: K and V straight into LDS, three
         // workgroups per CU.
         const dim3 grid(nh, B), block(256);
         if (head_dim == 32)
-            hipLaunchKernelGGL(attention_bf16_short_kernel<32>, grid, block, 0, s, qkv, cu_seqlens, ctx, H, scale);
+            hipLaunchKernelGGL(attention_bf16_short_kernel<32>, grid, block, 0, s, qkv, cu_seqlens, ctx, H, scale, order);
         else if (head_dim == 64)
-            hipLaunchKernelGGL(attention_bf16_short_kernel<64>, grid, block, 0, s, qkv, cu_seqlens, ctx, H, scale);
+            hipLaunchKernelGGL(attention_bf16_short_kernel<64>, grid, block, 0, s, qkv, cu_seqlens, ctx, H, scale, order);
         else
             return hipErrorInvalidValue;
         return hipGetLastError();
     }
     const dim3 grid(nh, (max_len + 127) / 128, B), block(256);
     if (head_dim == 32)
-        hipLaunchKernelGGL(attention_bf16_kernel<32>, grid, block, 0, s, qkv, cu_seqlens, ctx, H, scale);
+        hipLaunchKernelGGL(attention_bf16_kernel<32>, grid, block, 0, s, qkv, cu_seqlens, ctx, H, scale, order);
     else if (head_dim == 64)
-        hipLaunchKernelGGL(attention_bf16_kernel<64>, grid, block, 0, s, qkv, cu_seqlens, ctx, H, scale);
+        hipLaunchKernelGGL(attention_bf16_kernel<64>, grid, block, 0, s, qkv, cu_seqlens, ctx, H, scale, order);
     else
         return hipErrorInvalidValue;
     return hipGetLastError();
 }
 
 hipError_t launch_attention(const float* qkv, const int* cu_seqlens, int B, int max_len, int H,
-                            int nh, int head_dim, float scale, float* ctx, hipStream_t s) {
+                            int nh, int head_dim, float scale, float* ctx, hipStream_t s, const int* order) {
     if (B <= 0 || max_len <= 0) return hipSuccess;
     const dim3 grid(nh, (max_len + 127) / 128, B), block(256);
     if (head_dim == 32)
-        hipLaunchKernelGGL(attention_kernel<32>, grid, block, 0, s, qkv, cu_seqlens, ctx, H, scale);
+        hipLaunchKernelGGL(attention_kernel<32>, grid, block, 0, s, qkv, cu_seqlens, ctx, H, scale, order);
     else if (head_dim == 64)
-        hipLaunchKernelGGL(attention_kernel<64>, grid, block, 0, s, qkv, cu_seqlens, ctx, H, scale);
+        hipLaunchKernelGGL(attention_kernel<64>, grid, block, 0, s, qkv, cu_seqlens, ctx, H, scale, order);
     else
         return hipErrorInvalidValue;
     return hipGetLastError();

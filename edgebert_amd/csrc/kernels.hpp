@@ -56,15 +56,18 @@ hipError_t launch_gemm_f32(const GemmArgs& a, int epi, hipStream_t s);
 hipError_t launch_gemm_bf16(const GemmArgs& a, int epi, hipStream_t s);
 
 // Masked multi-head attention over packed sequences: qkv [T, 3H] rows
-// (q | k | v), cu_seqlens [B+1]; ctx [T, H].  head_dim 32 or 64.
+// (q | k | v), cu_seqlens [B+1]; ctx [T, H].  head_dim 32 or 64.  order
+// (nullable): a permutation of the B sequences, the order in which the grid
+// takes them (launch_pack writes one by decreasing length).
 hipError_t launch_attention(const float* qkv, const int* cu_seqlens, int B, int max_len,
-                            int H, int nh, int head_dim, float scale, float* ctx, hipStream_t s);
+                            int H, int nh, int head_dim, float scale, float* ctx, hipStream_t s,
+                            const int* order = nullptr);
 
 // Attention with bf16 q / k / v (qkv [T, 3H] bf16 bits) and bf16 context;
 // scores, softmax and accumulation in fp32.  head_dim 32 or 64.
 hipError_t launch_attention_bf16(const uint16_t* qkv, const int* cu_seqlens, int B, int max_len,
                                  int H, int nh, int head_dim, float scale, uint16_t* ctx,
-                                 hipStream_t s);
+                                 hipStream_t s, const int* order = nullptr);
 
 // C = LayerNorm((A . W^T + bias) + R) per row (fp32), C may alias R (each
 // element is read and written by the same lane).  One workgroup owns whole rows
@@ -102,9 +105,10 @@ hipError_t launch_add_layernorm_y16(const uint16_t* y, const float* bias, float*
                                     const float* b, int rows_max, const int* rows_dev, int H, float eps,
                                     uint16_t* x16, hipStream_t s);
 
-// Token packing: mask [B,S] -> cu_seqlens [B+1], n_tokens, packed ids/positions.
+// Token packing: mask [B,S] -> cu_seqlens [B+1], n_tokens, packed ids/positions;
+// with `order` (B ints), also the sequences by decreasing length.
 hipError_t launch_pack(const int* ids, const int* mask, int B, int S, int* counts, int* cu,
-                       int* n_tokens, int* tok_id, int* tok_pos, hipStream_t s);
+                       int* n_tokens, int* tok_id, int* tok_pos, hipStream_t s, int* order = nullptr);
 
 // n 32-bit words at p set to zero (a kernel launch, never a memset node).
 hipError_t launch_zero_words(void* p, int64_t n, hipStream_t s);

@@ -35,10 +35,17 @@ __global__ __launch_bounds__(256) void pack_count_kernel(const int* __restrict__
 }
 
 // Exclusive scan of counts[0..B) -> cu[0..B], n_tokens = cu[B]; one workgroup.
+// With `order`, also the sequences by decreasing length (a counting sort over
+// the lengths, clamped to ORDER_BINS - 1; ties in any order): the attention
+// grid walks them longest first, so that the long sequences' workgroups start
+// first and the short ones fill in around them.
+constexpr int ORDER_BINS = 1024;
 __global__ __launch_bounds__(1024) void pack_scan_kernel(const int* __restrict__ counts, int B,
                                                          int* __restrict__ cu,
-                                                         int* __restrict__ n_tokens) {
+                                                         int* __restrict__ n_tokens,
+                                                         int* __restrict__ order) {
     __shared__ int buf[1024];
+    __shared__ int next[ORDER_BINS];
     const int tid = threadIdx.x;
     const int per = (B + 1023) / 1024;
     const int lo = min(B, tid * per), hi = min(B, lo + per);
@@ -61,6 +68,26 @@ __global__ __launch_bounds__(1024) void pack_scan_kernel(const int* __restrict__
         cu[B] = buf[1023];
         *n_tokens = buf[1023];
     }
+    if (!order) return;   // uniform over the workgroup
+    static_assert(ORDER_BINS == 1024, "one bin per thread");
+    next[tid] = 0;
+    __syncthreads();
+    for (int b = tid; b < B; b += 1024) atomicAdd(&next[min(counts[b], ORDER_BINS - 1)], 1);
+    __syncthreads();
+    // Thread t takes bin 1023 - t, so the inclusive scan runs from the
+    // longest length down; its exclusive value is the bin's first slot.
+    const int n_bin = next[ORDER_BINS - 1 - tid];
+    buf[tid] = n_bin;
+    __syncthreads();
+    for (int off = 1; off < 1024; off <<= 1) {
+        const int v = tid >= off ? buf[tid - off] : 0;
+        __syncthreads();
+        buf[tid] += v;
+        __syncthreads();
+    }
+    next[ORDER_BINS - 1 - tid] = buf[tid] - n_bin;
+    __syncthreads();
+    for (int b = tid; b < B; b += 1024) order[atomicAdd(&next[min(counts[b], ORDER_BINS - 1)], 1)] = b;
 }
 
 __global__ __launch_bounds__(256) void pack_scatter_kernel(const int* __restrict__ ids,
@@ -92,10 +119,10 @@ __global__ __launch_bounds__(256) void pack_scatter_kernel(const int* __restrict
 }
 
 hipError_t launch_pack(const int* ids, const int* mask, int B, int S, int* counts, int* cu,
-                       int* n_tokens, int* tok_id, int* tok_pos, hipStream_t s) {
+                       int* n_tokens, int* tok_id, int* tok_pos, hipStream_t s, int* order) {
     if (B <= 0) return hipSuccess;
     hipLaunchKernelGGL(pack_count_kernel, dim3(B), dim3(256), 0, s, mask, S, counts);
-    hipLaunchKernelGGL(pack_scan_kernel, dim3(1), dim3(1024), 0, s, counts, B, cu, n_tokens);
+    hipLaunchKernelGGL(pack_scan_kernel, dim3(1), dim3(1024), 0, s, counts, B, cu, n_tokens, order);
     hipLaunchKernelGGL(pack_scatter_kernel, dim3(B), dim3(256), 0, s, ids, mask, S, cu, tok_id,
                        tok_pos);
     return hipGetLastError();
