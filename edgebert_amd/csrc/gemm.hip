@@ -333,6 +333,14 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_persistent_kernel
     if (total == 0) return;  // uniform over the workgroup
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    // fp32 products take the wave index as a wave-uniform (scalar) value, so
+    // that the k-loop's LDS destinations come from scalar arithmetic: fp32
+    // MFMAs hold the SIMD's VALU while they run, and VALU address math in
+    // the k-loop adds to the MFMA time (c3: QKV 233.7 -> 225.6 us, FFN up
+    // 306.7 -> 298.2 us).  bf16 MFMAs leave the VALU free, and there the
+    // scalar form was slower (c5 GEMMs +3-4%), as it was for the split
+    // products; the LayerNorm instances' epilogue needs the SGPRs.
+    const int wave_u = LN || BF16 || SPLIT6 ? wave : __builtin_amdgcn_readfirstlane(wave);
     const int wm = wave / WAVES_N, wn = wave % WAVES_N;
     const int l32 = lane & 31, half = lane >> 5;
     const char* __restrict__ A = static_cast<const char*>(p.A);
@@ -388,7 +396,7 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_persistent_kernel
         for (int i = 0; i < NL; ++i)
             if (i / PER == part)
                 load_lds16_sbase(i < LA ? abase : wbase, soff[i],
-                                 st + (i < LA ? 0 : BM * RW) + ((i < LA ? i : i - LA) * NT + wave * 64) * 4);
+                                 st + (i < LA ? 0 : BM * RW) + ((i < LA ? i : i - LA) * NT + wave_u * 64) * 4);
         if (part == NPART - 1) {
             if (HAS_BIAS && nit % nk == 0)
                 load_lds16_async(bias_src, smem + NSTAGE * STAGE + (((nit / nk) & 1) * NW + wave) * BIAS_SLOT);
