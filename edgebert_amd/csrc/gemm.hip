@@ -390,13 +390,24 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_persistent_kernel
     // bias chunk and moves on to the next k-tile.
     constexpr int NPART = KS > 1 ? KS / 2 : 1;
     constexpr int PER = (NL + NPART - 1) / NPART;
+    // LDS destinations: fp32 products form them as 32-bit integers (no
+    // generic 64-bit LDS pointer, fewer VALU instructions in the k-loop:
+    // FFN down 297.2 -> 289.2 us at c3); the bf16 and split products keep
+    // the pointer form, which measured faster there (c5 GEMMs 3-5%).
+    const uint32_t lds_wave = (uint32_t)(uintptr_t)smem + (uint32_t)wave_u * 64 * 16;
     auto issue_part = [&](int part) {
-        float* st = smem + (nit % NSTAGE) * STAGE;
+        const uint32_t st = lds_wave + (uint32_t)((nit % NSTAGE) * STAGE) * 4;
+        float* stp = smem + (nit % NSTAGE) * STAGE;
 #pragma unroll
         for (int i = 0; i < NL; ++i)
-            if (i / PER == part)
-                load_lds16_sbase(i < LA ? abase : wbase, soff[i],
-                                 st + (i < LA ? 0 : BM * RW) + ((i < LA ? i : i - LA) * NT + wave_u * 64) * 4);
+            if (i / PER == part) {
+                if constexpr (BF16 || SPLIT6)
+                    load_lds16_sbase(i < LA ? abase : wbase, soff[i],
+                                     stp + (i < LA ? 0 : BM * RW) + ((i < LA ? i : i - LA) * NT + wave * 64) * 4);
+                else
+                    load_lds16_sbase(i < LA ? abase : wbase, soff[i],
+                                     st + (uint32_t)((i < LA ? 0 : BM * RW) + (i < LA ? i : i - LA) * NT * 4) * 4);
+            }
         if (part == NPART - 1) {
             if (HAS_BIAS && nit % nk == 0)
                 load_lds16_async(bias_src, smem + NSTAGE * STAGE + (((nit / nk) & 1) * NW + wave) * BIAS_SLOT);

@@ -260,9 +260,10 @@ __device__ __forceinline__ uint64_t uniform_u64(const void* p) {
 
 // load_lds16_async with the global address split as a wave-uniform 64-bit
 // base (SGPR pair) plus this lane's 32-bit byte offset: the saddr form of
-// global_load_lds_dwordx4.
-__device__ __forceinline__ void load_lds16_sbase(uint64_t sbase, uint32_t voff, const float* lds) {
-    const uint32_t base = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)lds);
+// global_load_lds_dwordx4.  lds_addr is the LDS byte address (the same for
+// every lane).
+__device__ __forceinline__ void load_lds16_sbase(uint64_t sbase, uint32_t voff, uint32_t lds_addr) {
+    const uint32_t base = __builtin_amdgcn_readfirstlane(lds_addr);
     const void* sb = (const void*)(uintptr_t)sbase;
     uint32_t saved;
     asm volatile(
@@ -274,6 +275,9 @@ __device__ __forceinline__ void load_lds16_sbase(uint64_t sbase, uint32_t voff, 
         : "=&s"(saved)
         : "v"(voff), "s"(sb), "s"(base)
         : "memory");
+}
+__device__ __forceinline__ void load_lds16_sbase(uint64_t sbase, uint32_t voff, const float* lds) {
+    load_lds16_sbase(sbase, voff, (uint32_t)(uintptr_t)lds);
 }
 
 // At most n vector-memory operations of this wave outstanding (n is
