@@ -137,6 +137,29 @@ def test_large_ragged_batch_takes_the_fused_paths(eb, oracle_mod, weights_for):
     assert err <= FP32_MAX_ABS and cos >= FP32_MIN_COS
 
 
+def test_many_ragged_sequences_any_batch_order(eb, oracle_mod, weights_for):
+    """1,500 sequences of 1..40 tokens: more sequences than the packing scan's
+    workgroup has threads, so its length sort (the order the attention grid
+    takes the sequences in) walks the batch in strides, with many equal
+    lengths.  Every row unit-norm, 25 sequences against the oracle, and a
+    permuted batch gives the permuted rows bit for bit (each sequence's vector
+    depends on that sequence only, whichever workgroup computes it)."""
+    from edgebert_amd.synth import InputSpec, MINILM_L6, make_inputs
+    spec = InputSpec("ragged1500", MINILM_L6, 1500, 40, 1, 40, 5)
+    w = weights_for(spec.model)
+    ids, mask, lengths = make_inputs(spec)
+    m = gpu_model(eb, spec.model, w)
+    got = m.encode_ids(ids, mask, normalize=True)
+    np.testing.assert_allclose(np.linalg.norm(got.astype(np.float64), axis=1), 1.0, atol=1e-5)
+    sel = np.arange(0, spec.batch, spec.batch // 25)[:25]
+    want = oracle_mod.OracleModel(spec.model, w).encode_unpadded(ids[sel], mask[sel], normalize=True)
+    err, cos = _report("ragged 1500 subsample", got[sel], want)
+    assert err <= FP32_MAX_ABS and cos >= FP32_MIN_COS
+    perm = np.random.default_rng(3).permutation(spec.batch)
+    got_p = m.encode_ids(np.ascontiguousarray(ids[perm]), np.ascontiguousarray(mask[perm]), normalize=True)
+    assert np.array_equal(got_p, got[perm])
+
+
 def test_bert_base_fp32_few_tokens_split_k(eb, oracle_mod, weights_for):
     """BERT-base in fp32 with 3 short sentences: the bias-free projections are
     split over K (6 splits at K = 768, 8 at K = 3072) into partial products
