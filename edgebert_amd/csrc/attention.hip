@@ -11,7 +11,10 @@
 //
 // Work split: workgroup = (head, 128-query block, sequence), 4 waves of 32
 // queries.  K and V of the sequence stream through LDS in 128-key chunks;
-// softmax is online across chunks (one chunk when S <= 128).
+// softmax is online across chunks (one chunk when S <= 128).  The grid's
+// sequence index goes through `order` when the caller has one (the packing
+// scan writes the sequences longest first), so that the long sequences'
+// workgroups start first.
 //
 // Transposed scores: each wave computes S^T = K . Q^T with
 // v_mfma_f32_32x32x2_f32, so lane l owns query l%32 and, for each 32-key
