@@ -340,6 +340,9 @@ def attention64(qkv, cu, H, nh):
     (384, 12, [256, 300, 511, 512]),
     (768, 12, [1, 64, 128, 130, 257]),
     (64, 2, [5, 17]),
+    # at most 128 tokens: 64-key chunks, the second one prefetched
+    (384, 12, [1, 63, 64, 65, 100, 127, 128]),
+    (768, 12, [1, 65, 128]),
 ])
 def test_attention(env, H, nh, lengths):
     torch, eb, Nn, L = env
