@@ -456,6 +456,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
     constexpr int NS = HD / 16;             // 16-dim slices of q.k
     __shared__ __attribute__((aligned(16))) uint16_t Ks[TILE];
     __shared__ __attribute__((aligned(16))) uint16_t Vs[TILE];
+    __shared__ __attribute__((aligned(16))) uint16_t Qs[TILE];
 
     const int head = blockIdx.x, b = order ? order[blockIdx.y] : (int)blockIdx.y;
     const int start = cu_seqlens[b];
@@ -468,10 +469,19 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
     const uint16_t* Kg = Qg + H;
     const uint16_t* Vg = Qg + 2 * H;
 
-    // K and V into LDS: wave w's load i fills 16-byte slots (4 i + w) * 64 +
-    // lane, i.e. row P / CPR, stored chunk P % CPR.  Rows past the sequence
-    // re-read its last row (their keys are masked, their V rows meet zero
-    // probabilities).
+    // Q, K and V into LDS, in that order: wave w's load i fills 16-byte slots
+    // (4 i + w) * 64 + lane, i.e. row P / CPR, stored chunk P % CPR.  Rows
+    // past the sequence re-read its last row (their keys are masked, their V
+    // rows meet zero probabilities, their queries are not stored).  The scores
+    // wait for Q and K only; V lands while they and the softmax run.
+#pragma unroll
+    for (int i = 0; i < NLD; ++i) {
+        const int P = (i * 4 + wave) * 64 + lane;
+        const int r = P / CPR, pc = P % CPR;
+        const int64_t row = (int64_t)min(r, len - 1) * ld;
+        load_lds16_async(Qg + row + 8 * (pc ^ chunk_swizzle16<CPR>(r)),
+                         reinterpret_cast<const float*>(Qs + (i * 4 + wave) * 512));
+    }
 #pragma unroll
     for (int i = 0; i < NLD; ++i) {
         const int P = (i * 4 + wave) * 64 + lane;
@@ -479,17 +489,23 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
         const int64_t row = (int64_t)min(r, len - 1) * ld;
         load_lds16_async(Kg + row + 8 * (pc ^ chunk_swizzle16<CPR>(r)),
                          reinterpret_cast<const float*>(Ks + (i * 4 + wave) * 512));
+    }
+#pragma unroll
+    for (int i = 0; i < NLD; ++i) {
+        const int P = (i * 4 + wave) * 64 + lane;
+        const int r = P / CPR, pc = P % CPR;
+        const int64_t row = (int64_t)min(r, len - 1) * ld;
         load_lds16_async(Vg + row + 8 * (pc ^ v_swizzle<HD>(r)),
                          reinterpret_cast<const float*>(Vs + (i * 4 + wave) * 512));
     }
+    wait_vmcnt(NLD);   // this wave's Q and K loads (its V loads may be in flight)
+    __syncthreads();
     // This lane's query as the B operand: dims 16s + 8*half .. +7.
-    const int qi = min(wave * 32 + l32, len - 1);
+    const int qr = wave * 32 + l32;
     v8s_t qf[NS];
 #pragma unroll
     for (int s = 0; s < NS; ++s)
-        qf[s] = *reinterpret_cast<const v8s_t*>(Qg + (int64_t)qi * ld + 16 * s + 8 * half);
-    wait_vmcnt(0);
-    __syncthreads();
+        qf[s] = *reinterpret_cast<const v8s_t*>(Qs + qr * HD + 8 * ((2 * s + half) ^ chunk_swizzle16<CPR>(qr)));
 
     const int nkb = (len + 31) / 32;     // 32-key blocks holding real keys
     // S^T = K . Q^T: the four 32-key blocks' MFMA chains side by side.
@@ -545,6 +561,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
     for (int j = 0; j < NJ; ++j)
 #pragma unroll
         for (int r = 0; r < 16; ++r) o[j][r] = 0.0f;
+    wait_vmcnt(0);     // this wave's V loads
+    __syncthreads();   // and everyone else's
     // context^T += V^T . P^T, two 16-key MFMAs per 32-key block.  Lane half h
     // of the B operand (P) holds keys 16 mm + 4 h + 0..3 and 16 mm + 8 + 4 h +
     // 0..3; the A operand (V^T) gets the same keys at dim l32 from two
