@@ -36,10 +36,10 @@ namespace ebh {
 typedef float v16f __attribute__((ext_vector_type(16)));
 typedef float v4f __attribute__((ext_vector_type(4)));
 
-// One 128-key chunk of the fp32 kernel below for the wave's 32 queries:
-// S^T = K . Q^T, the key-padding mask, the online-softmax update and
-// context^T += V^T . P^T.  lim = real keys in the chunk (1..128); c2 = scale
-// log2(e).  Fewer VALU instructions matter here: on this chip the VALU does
+// One key chunk (up to 128 keys, in 32-key blocks) of the fp32 kernel below
+// for the wave's 32 queries: S^T = K . Q^T, the key-padding mask, the
+// online-softmax update and context^T += V^T . P^T.  lim = real keys in the
+// chunk (1..128); c2 = scale log2(e).  Fewer VALU instructions matter here: on this chip the VALU does
 // not issue while an fp32 MFMA of the same SIMD runs, so the softmax's
 // instructions add to the MFMA time instead of hiding behind it.
 template <int HD>
@@ -420,11 +420,11 @@ __global__ __launch_bounds__(256) void attention_bf16_kernel(const uint16_t* __r
 
 // ---------------------------------------------------------------------------
 // bf16 attention for sequences of at most 128 tokens: one key chunk and one
-// query block per (head, sequence) workgroup.  K and V go straight from HBM
-// into LDS (global_load_lds_dwordx4, no staging registers, no transposing
-// copy), so a workgroup needs 32 KB of LDS and about 150 VGPRs: three
+// query block per (head, sequence) workgroup.  Q, K and V go straight from
+// HBM into LDS (global_load_lds_dwordx4, no staging registers, no transposing
+// copy), so a workgroup needs 48 KB of LDS and at most 110 VGPRs: three
 // workgroups per CU, whose load phases overlap each other's MFMAs and
-// softmax.
+// softmax; within a workgroup the scores wait for Q and K only.
 //
 // K rows sit unpadded with 16-byte chunk c of row r at c ^ chunk_swizzle16(r)
 // (conflict-free fragment reads down 32 rows), as the GEMM tiles do.  V stays
