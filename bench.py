@@ -24,6 +24,13 @@ texts are the workload's ids spelled as words of a synthetic vocabulary, so
 they tokenise back to exactly those ids (``matches_ids``).  Beside it, the
 tokenisation alone, native and with the HF ``tokenizers`` library the
 reference uses.
+
+``kernels`` gives every kernel family of the headline forward the same way as
+``roofline`` (HIP events, fraction of its roofline).  ``configs`` holds the
+other BASELINE configs (c5, c4, c2, c1 by default), each timed after the
+headline with its own model exactly as the headline is (``value``,
+``ms_per_step``, p50), with its dominant kernel family as ``roofline`` and
+every family under ``kernels``; ``value`` and ``metric`` stay on c3.
 """
 from __future__ import annotations
 
@@ -269,6 +276,93 @@ def split_product_run(eb, torch, spec, weights, d_ids, d_mask, d_ref, lengths, s
                          "launches": launches}}
 
 
+LEG_DTYPE_NOTE = {
+    "fp32": "f32 (GEMM operands, accumulation, residual stream, LayerNorm, softmax)",
+    "bf16": "bf16 GEMM and attention operands with fp32 accumulation; bf16 residual stream "
+            "(the skip connection carries bf16-rounded values); LayerNorm statistics, softmax "
+            "and pooling in fp32",
+}
+
+
+def config_leg(eb, torch, name: str, steps: int, warmup: int, graph_replay: bool) -> dict:
+    """One BASELINE config timed as the headline is (forwards over HBM-resident
+    ids / mask, graph replay unless disabled), then every kernel family of its
+    forward timed with HIP events over as many forwards again (direct
+    launches), each as a fraction of its roofline: GEMMs and attention against
+    the matrix peak of the config's dtype, row kernels against HBM.  ``traffic``
+    is the committed counter summary's HBM bytes per launch, where one exists
+    for that config."""
+    spec = eb.CONFIGS[name]
+    cfg, dtype = spec.model, spec.dtype
+    weights = eb.make_weights(cfg)
+    ids, mask, lengths = eb.make_inputs(spec)
+    B, S = ids.shape
+    model = eb.Model.from_weights(weights, cfg, dtype)
+    del weights
+    if not graph_replay:
+        model.set_graph_replay(False)
+    dev = torch.device("cuda:0")
+    d_ids = torch.from_numpy(ids).to(dev)
+    d_mask = torch.from_numpy(mask).to(dev)
+    d_out = torch.empty((B, cfg.hidden_size), dtype=torch.float32, device=dev)
+    stream = torch.cuda.current_stream(dev).cuda_stream
+
+    def step():
+        model.encode_device(d_ids.data_ptr(), d_mask.data_ptr(), B, S, d_out.data_ptr(), True, stream)
+
+    for _ in range(warmup):
+        step()
+    model.synchronize()
+    torch.cuda.synchronize()
+    times = []
+    t_all = time.perf_counter()
+    for _ in range(steps):
+        t0 = time.perf_counter()
+        step()
+        torch.cuda.synchronize()
+        times.append(time.perf_counter() - t0)
+    wall = time.perf_counter() - t_all
+    model.synchronize()
+    fused = few_fused(cfg, B, S, dtype)
+    families = {}
+    for fam in KERNELS:
+        if fused and fam == "gemm_out":
+            continue
+        model.profile_enable(fam)
+        for _ in range(steps):
+            step()
+        model.synchronize()
+        torch.cuda.synchronize()
+        launches, prof_ms = model.profile_read()
+        model.profile_enable("none")
+        if not launches:
+            continue
+        avg = prof_ms / launches
+        work, bound, wunit = kernel_work(cfg, lengths, B, fam, fused)
+        if bound == "mfma":
+            achieved, peak, punit = work / (avg * 1e-3) / 1e12, PEAK_TFLOPS[dtype], "TFLOP/s"
+        else:
+            achieved, peak, punit = work / (avg * 1e-3) / 1e9, HBM_PEAK_GBS, "GB/s"
+        families[fam] = {"bound": bound, "achieved": round(achieved, 3), "peak": peak, "unit": punit,
+                         "frac": round(achieved / peak, 4), "avg_launch_ms": round(avg, 5),
+                         "launches": launches, "per_forward": launches // steps,
+                         "traffic": measured_traffic(name, fam, dtype)}
+    model.close()
+    ms = 1e3 * wall / steps
+    top = max(families, key=lambda f: families[f]["avg_launch_ms"] * families[f]["per_forward"])
+    return {"value": round(B * steps / wall, 2), "unit": "sentences/s", "steps": steps, "warmup": warmup,
+            "ms_per_step": round(ms, 4), "p50_batch_latency_ms": round(float(np.median(times)) * 1e3, 4),
+            "dtype": LEG_DTYPE_NOTE[dtype],
+            "workload": f"{name}: {cfg.num_hidden_layers}L H{cfg.hidden_size} I{cfg.intermediate_size} "
+                        f"heads{cfg.num_attention_heads} batch {B} x seq {S}, lengths "
+                        f"{spec.len_lo}-{spec.len_hi}",
+            "valid_tokens": int(mask.sum()),
+            "forward_tflops": round(forward_flops(cfg, lengths) / (ms * 1e-3) / 1e12, 2),
+            "graph_replay": graph_replay,
+            "roofline": dict(kernel=top, **families[top]),
+            "kernels": families}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -289,6 +383,11 @@ def main():
                     help="batches timed for encode_texts and the tokenizers (0 disables)")
     ap.add_argument("--no-graph-replay", action="store_true",
                     help="run every forward as direct launches (no HIP graph replay)")
+    ap.add_argument("--legs", default=None,
+                    help="comma-separated BASELINE configs also timed, each with its own model, after "
+                         "the headline and reported under `configs` (default with --config c3: "
+                         "c5,c4,c2,c1; 'none' disables)")
+    ap.add_argument("--leg-steps", type=int, default=10, help="timed forwards per leg")
     ap.add_argument("--copy-probe-mb", type=int, default=0,
                     help="after the timed region, run 3 plain device copies of this many MiB "
                          "(the calibration dispatch for rocprofv3 FETCH_SIZE / WRITE_SIZE)")
@@ -418,10 +517,39 @@ def main():
         result["fp32_bf16x6"] = split_product_run(eb, torch, spec, weights, d_ids, d_mask, d_out, lengths,
                                                   x6_steps, args.warmup, args.profile_kernel,
                                                   not args.no_graph_replay)
+    # The headline's own kernel families, as the legs report theirs.
+    fams = {}
+    for fam in KERNELS:
+        if fused and fam == "gemm_out":
+            continue
+        model.profile_enable(fam)
+        timed(args.steps)
+        model.synchronize()
+        n, fms = model.profile_read()
+        model.profile_enable("none")
+        if n:
+            fwork, fbound, _ = kernel_work(cfg, lengths, B, fam, fused)
+            favg = fms / n
+            if fbound == "mfma":
+                fa, fp, fu = fwork / (favg * 1e-3) / 1e12, PEAK_TFLOPS[dtype], "TFLOP/s"
+            else:
+                fa, fp, fu = fwork / (favg * 1e-3) / 1e9, HBM_PEAK_GBS, "GB/s"
+            fams[fam] = {"bound": fbound, "achieved": round(fa, 3), "peak": fp, "unit": fu,
+                         "frac": round(fa / fp, 4), "avg_launch_ms": round(favg, 5), "launches": n,
+                         "traffic": measured_traffic(args.config, fam, dtype)}
+    result["kernels"] = fams
     if args.cpu_budget > 0:
         result["cpu_baseline"] = cpu_baseline(spec, weights, ids, mask, args.cpu_budget)
-    print(json.dumps(result), flush=True)
     model.close()
+    legs = args.legs if args.legs is not None else ("c5,c4,c2,c1" if args.config == "c3" else "none")
+    legs = [c for c in legs.split(",") if c and c != "none" and c != args.config]
+    if legs:
+        del weights
+        result["configs"] = {}
+        for name in legs:
+            result["configs"][name] = config_leg(eb, torch, name, args.leg_steps, args.warmup,
+                                                 not args.no_graph_replay)
+    print(json.dumps(result), flush=True)
 
 
 if __name__ == "__main__":

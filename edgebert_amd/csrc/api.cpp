@@ -805,9 +805,33 @@ int ebh_set_tensor(ebh_model* m, const char* name, const float* data, const int6
     return ebh::put_tensor(m, name, data, ebh::TENSOR_F32, shape, ndim, nullptr);
 }
 
+// Device resources a failed ebh_finalize had already made (stream, event,
+// weight block) are released and the model goes back to its state before the
+// call (host tensors kept), so the call can be repeated without leaking them.
+static void release_partial_finalize(ebh_model* m) {
+    if (m->device < 0) return;
+    (void)hipSetDevice(m->device);
+    if (m->stream) (void)hipStreamSynchronize(m->stream);
+    if (m->wbase) (void)hipFree(m->wbase);
+    if (m->done) (void)hipEventDestroy(m->done);
+    if (m->stream) (void)hipStreamDestroy(m->stream);
+    m->wbase = nullptr;
+    m->done = nullptr;
+    m->stream = nullptr;
+    m->device = -1;
+}
+
+static int finalize_locked(ebh_model* m, int32_t dtype);
+
 int ebh_finalize(ebh_model* m, int32_t dtype) {
     if (!m) return fail(EBH_ERR_INVALID_ARG, "null model");
     std::lock_guard<std::mutex> lk(m->mu);
+    const int rc = finalize_locked(m, dtype);
+    if (rc != EBH_OK && !m->finalized) release_partial_finalize(m);
+    return rc;
+}
+
+static int finalize_locked(ebh_model* m, int32_t dtype) {
     if (m->finalized) return fail(EBH_ERR_STATE, "model already finalized");
     if (dtype != EBH_DTYPE_F32 && dtype != EBH_DTYPE_BF16 && dtype != EBH_DTYPE_F32_BF16X6)
         return fail(EBH_ERR_INVALID_ARG, "unknown dtype %d", dtype);
@@ -1323,6 +1347,9 @@ int ebh_op_gemm_bf16(const uint16_t* A, int64_t lda, const uint16_t* W, int64_t 
         return fail(EBH_ERR_INVALID_ARG, "K must be a multiple of 64, N of 4, strides of 8 / 8 / 4");
     if (((uintptr_t)A | (uintptr_t)W | (uintptr_t)C | (uintptr_t)bias) & 15)
         return fail(EBH_ERR_INVALID_ARG, "operands must be 16-byte aligned");
+    if (!ebh::gemm_offsets_fit32(lda, ldw, 2))
+        return fail(EBH_ERR_INVALID_ARG, "row strides lda %lld / ldw %lld too large (at most %lld elements)",
+                    (long long)lda, (long long)ldw, (long long)ebh::gemm_stride_max(2));
     if (M == 0) return EBH_OK;
     ebh::GemmArgs a{};
     a.A = A; a.W = W; a.bias = bias; a.R = nullptr; a.C = static_cast<float*>(C);
@@ -1389,6 +1416,9 @@ int ebh_op_gemm_add_layer_norm(const float* A, int64_t lda, const float* W, int6
     if (!A || !W || !bias || !x || !gamma || !beta) return fail(EBH_ERR_INVALID_ARG, "null buffer");
     if (M < 0 || N != 384 || K <= 0 || K % 32 || lda < K || ldw < K || lda % 4 || ldw % 4)
         return fail(EBH_ERR_INVALID_ARG, "bad fused LayerNorm GEMM shape (N must be 384, K %% 32 == 0)");
+    if (!ebh::gemm_offsets_fit32(lda, ldw, 4))
+        return fail(EBH_ERR_INVALID_ARG, "row strides lda %lld / ldw %lld too large (at most %lld elements)",
+                    (long long)lda, (long long)ldw, (long long)ebh::gemm_stride_max(4));
     ebh::GemmArgs a{};
     a.A = A;
     a.W = W;

@@ -1230,7 +1230,7 @@ static bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
 hipError_t launch_gemm_f32(const GemmArgs& a, int epi, hipStream_t s) {
     const bool ok = epi != EPI_BIAS_RESID && aligned16(a.A) && aligned16(a.W) && aligned16(a.C) &&
                     (epi == EPI_NONE || aligned16(a.bias)) && a.lda % 4 == 0 && a.ldw % 4 == 0 &&
-                    a.ldc % 4 == 0 && a.N % 4 == 0;
+                    a.ldc % 4 == 0 && a.N % 4 == 0 && gemm_offsets_fit32(a.lda, a.ldw, 4);
     // Tile choice measured on MI355X at MiniLM shapes (M = 2.4k .. 32k tokens):
     //  * few tokens (under half a 128 x 128 tile per CU, e.g. the narrow
     //    projections of batch 32 of short sentences): 64 x 64 tiles, two
@@ -1325,7 +1325,8 @@ bool gemm_f32_add_ln_fits(int M_max, int N, int K) {
 hipError_t launch_gemm_f32_add_ln(const GemmArgs& a, hipStream_t s) {
     const bool ok = a.N == ADD_LN_BN && a.K % ADD_LN_BK == 0 && a.K >= ADD_LN_BK && a.splits <= 1 &&
                     aligned16(a.A) && aligned16(a.W) && aligned16(a.bias) && a.R && a.C && a.ln_g &&
-                    a.ln_b && a.lda % 4 == 0 && a.ldw % 4 == 0 && a.M_max >= 0;
+                    a.ln_b && a.lda % 4 == 0 && a.ldw % 4 == 0 && a.M_max >= 0 &&
+                    gemm_offsets_fit32(a.lda, a.ldw, 4);
     if (!ok) return hipErrorInvalidValue;
     const int tiles = (a.M_max + ADD_LN_BM - 1) / ADD_LN_BM;
     if (tiles == 0) return hipSuccess;
@@ -1344,7 +1345,8 @@ hipError_t launch_gemm_f32_add_ln(const GemmArgs& a, hipStream_t s) {
 hipError_t launch_gemm_bf16_act(const GemmArgs& a, int epi, bool c_bf16, hipStream_t s) {
     const bool ok = epi != EPI_BIAS_RESID && a.splits <= 1 && aligned16(a.A) && aligned16(a.W) && aligned16(a.C) &&
                     (epi == EPI_NONE || aligned16(a.bias)) && a.lda % 8 == 0 && a.ldw % 8 == 0 &&
-                    a.ldc % 4 == 0 && a.N % 4 == 0 && a.K % 64 == 0 && a.K > 0;
+                    a.ldc % 4 == 0 && a.N % 4 == 0 && a.K % 64 == 0 && a.K > 0 &&
+                    gemm_offsets_fit32(a.lda, a.ldw, 2);
     if (!ok) return hipErrorInvalidValue;
     if (c_bf16) return launch_persistent<256, 256, 64, 2, 4, 2, true, true>(a, epi, s, 1);
     return launch_persistent<256, 256, 64, 2, 4, 2, true, false>(a, epi, s, 1);

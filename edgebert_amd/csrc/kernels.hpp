@@ -38,6 +38,24 @@ struct GemmArgs {
     int split6;
 };
 
+// The persistent GEMM kernels address each k-tile load as a per-tile base
+// plus a 32-bit lane offset, (row within the tile) * stride * element size
+// plus the k-chunk.  Their tiles span at most GEMM_TILE_ROWS_MAX rows of A or
+// W, so row strides (lda, ldw, in elements of es bytes) must keep that offset
+// below 2^32; launch_gemm_f32 sends larger strides to the guarded kernel
+// (64-bit addresses), the other persistent launchers reject them.
+constexpr int GEMM_TILE_ROWS_MAX = 384;
+// Largest row stride (elements of es bytes) the persistent kernels take:
+// GEMM_TILE_ROWS_MAX * stride * es + (one k-tile of at most 64 elements) * es
+// stays below 2^32.
+inline int64_t gemm_stride_max(int es) {
+    return ((int64_t(1) << 32) - 1 - 64 * es) / (GEMM_TILE_ROWS_MAX * es);
+}
+inline bool gemm_offsets_fit32(int64_t lda, int64_t ldw, int es) {
+    const int64_t ld = lda > ldw ? lda : ldw;
+    return ld >= 0 && ld <= gemm_stride_max(es);
+}
+
 // The few-token GEMM path: M_max <= SKINNY_MAX_ROWS rows in 16-row blocks,
 // N % 32 == 0, K % 64 == 0, 16-byte aligned rows and operands.
 constexpr int SKINNY_MAX_ROWS = 64;

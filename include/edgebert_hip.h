@@ -97,7 +97,8 @@ EBH_API int ebh_set_tensor(ebh_model* m, const char* name, const float* data, co
  * (F32 into fp32 slots; BF16 GEMM weights straight into a bf16 model's
  * weights; anything else converted on the device: F16 / BF16 -> fp32 exactly,
  * F16 / F32 -> bf16 rounded to nearest even).  The file must stay unchanged
- * until ebh_finalize or ebh_destroy releases the mapping.  A
+ * until ebh_finalize or ebh_destroy releases the mapping: a file truncated
+ * in place meanwhile makes the upload's reads raise SIGBUS.  A
  * classifier.weight / classifier.bias pair is loaded as the cross-encoder
  * head; other tensors the encoder does not use (pooler.*) are skipped. */
 EBH_API int ebh_load_safetensors(ebh_model* m, const char* path);

@@ -34,7 +34,9 @@ extern "C" {
  * EBH_DTYPE_F32_BF16X6: fp32 W, products formed as six bf16 MFMA products of
  * three-way bf16 splits of A and W (see edgebert_hip.h).  C [M, N] (ldc);
  * residual [M, N] (ldr) only for EBH_EPI_BIAS_RESID; bias may be NULL for EBH_EPI_NONE.  K and the strides must
- * be multiples of 4 (fp32) / 8 (bf16). */
+ * be multiples of 4 (fp32) / 8 (bf16).  fp32 row strides above 2,796,202
+ * elements run on the guarded kernel (64-bit addresses) instead of the
+ * persistent ones, whose lane offsets are 32-bit. */
 EBH_API int ebh_op_gemm(const float* A, int64_t lda, const void* W, int64_t ldw, int32_t w_dtype,
                 const float* bias, const float* residual, int64_t ldr, float* C, int64_t ldc,
                 int32_t M, int32_t N, int32_t K, int32_t epilogue, void* stream);
@@ -43,7 +45,9 @@ EBH_API int ebh_op_gemm(const float* A, int64_t lda, const void* W, int64_t ldw,
  * accumulate, C [M, N] fp32 (c_dtype EBH_DTYPE_F32) or bf16 bits
  * (EBH_DTYPE_BF16), epilogue EBH_EPI_BIAS / EBH_EPI_BIAS_GELU / EBH_EPI_NONE.
  * K % 64 == 0, N % 4 == 0, strides of 8 / 8 / 4 elements, 16-byte aligned
- * operands.  The forward of EBH_DTYPE_BF16 models uses it for every Linear. */
+ * operands, lda and ldw at most 5,592,405 elements (the kernel's 32-bit lane
+ * offsets span 384 rows of a stride; EBH_ERR_INVALID_ARG beyond).  The forward
+ * of EBH_DTYPE_BF16 models uses it for every Linear. */
 EBH_API int ebh_op_gemm_bf16(const uint16_t* A, int64_t lda, const uint16_t* W, int64_t ldw,
                      const float* bias, void* C, int64_t ldc, int32_t c_dtype, int32_t M, int32_t N,
                      int32_t K, int32_t epilogue, void* stream);
@@ -79,8 +83,9 @@ EBH_API int ebh_op_add_layer_norm(const float* y, const float* bias, float* x, c
  * 677-679 with the Linear of 732-733 / 741-747): x = LayerNorm((A.W^T + bias)
  * + x), in place on x [M, N] (row stride N), A [M, K] fp32 (lda), W [N, K] fp32
  * (ldw).  Each 128-row block is one workgroup that holds whole rows, so N must
- * be 384 (the MiniLM width); K % 32 == 0, strides multiples of 4, A, W and
- * bias 16-byte aligned.  Same result, within fp32 rounding, as ebh_op_gemm
+ * be 384 (the MiniLM width); K % 32 == 0, strides multiples of 4 and at
+ * most 2,796,202 elements (32-bit lane offsets over 384 rows;
+ * EBH_ERR_INVALID_ARG beyond), A, W and bias 16-byte aligned.  Same result, within fp32 rounding, as ebh_op_gemm
  * (EBH_EPI_NONE) followed by ebh_op_add_layer_norm; the fp32 forward uses it
  * when there are at least as many 128-row blocks as CUs. */
 EBH_API int ebh_op_gemm_add_layer_norm(const float* A, int64_t lda, const float* W, int64_t ldw,

@@ -155,6 +155,31 @@ def test_op_entry_points_validate_before_launch(L):
     assert L.ebh_op_f32_to_bf16(p, p, -1, nul) == N.EBH_ERR_INVALID_ARG
 
 
+def test_gemm_ops_reject_strides_past_32bit_lane_offsets(L):
+    """The persistent GEMM kernels address a k-tile load as a per-tile base plus
+    a 32-bit lane offset of up to 384 rows of a stride: the bf16 op and the
+    fused LayerNorm op refuse strides whose offsets would wrap, naming them,
+    before any launch (fp32 ebh_op_gemm runs such strides on its guarded
+    64-bit kernel instead)."""
+    buf = np.zeros(256, np.float32)
+    base = buf.ctypes.data
+    p = ctypes.c_void_p(base + (-base) % 16)
+    nul = None
+    max16, max32 = 5_592_405, 2_796_202
+    assert (max16 + 1) * 384 * 2 + 64 * 2 > 2 ** 32 >= max16 * 384 * 2 + 64 * 2
+    assert (max32 + 1) * 384 * 4 + 64 * 4 > 2 ** 32 >= max32 * 384 * 4 + 64 * 4
+    big16 = max16 + 3          # the next multiple of 8
+    rc = L.ebh_op_gemm_bf16(p, big16, p, 64, p, p, 256, 1, 1, 256, 64, 0, nul)
+    assert rc == N.EBH_ERR_INVALID_ARG and "too large" in N.last_error()
+    rc = L.ebh_op_gemm_bf16(p, 64, p, big16, p, p, 256, 1, 1, 256, 64, 0, nul)
+    assert rc == N.EBH_ERR_INVALID_ARG and "too large" in N.last_error()
+    big32 = max32 + 2          # the next multiple of 4
+    rc = L.ebh_op_gemm_add_layer_norm(p, big32, p, 32, p, p, p, p, 1, 384, 32, 1e-12, nul)
+    assert rc == N.EBH_ERR_INVALID_ARG and "too large" in N.last_error()
+    rc = L.ebh_op_gemm_add_layer_norm(p, 32, p, big32, p, p, p, p, 1, 384, 32, 1e-12, nul)
+    assert rc == N.EBH_ERR_INVALID_ARG and "too large" in N.last_error()
+
+
 # ---------------------------------------------------------------------------
 # safetensors (ModelWeights::load, src/weights.rs:15-45)
 # ---------------------------------------------------------------------------

@@ -79,6 +79,32 @@ def test_gemm_f32(env, M, N, K, epi):
     np.testing.assert_allclose(got, want, rtol=0, atol=tol)
 
 
+def test_gemm_f32_row_stride_past_32bit_offsets(env):
+    """A rows 17.1M floats apart (a 4.4 GB operand): 63 rows of that stride lie
+    past 2^32 bytes, beyond the 32-bit lane offsets of the persistent kernels'
+    64-row tiles that this shape would otherwise take, so the op runs the
+    guarded kernel (64-bit addresses).  Against the float64 product of the rows
+    used."""
+    torch, eb, Nn, L = env
+    M, N, K, lda = 65, 128, 64, 17_100_000
+    assert 63 * lda * 4 >= 2 ** 32
+    rng = np.random.default_rng(17)
+    A = rng.standard_normal((M, K)).astype(np.float32)
+    W = (0.05 * rng.standard_normal((N, K))).astype(np.float32)
+    bias = rng.standard_normal(N).astype(np.float32)
+    big = torch.zeros(M * lda, device="cuda")
+    big.view(M, lda)[:, :K] = torch.from_numpy(A).cuda()
+    dW, db = dev(torch, W), dev(torch, bias)
+    dC = torch.full((M, N), float("nan"), device="cuda")
+    Nn.check(L.ebh_op_gemm(vp(big), lda, vp(dW), K, Nn.EBH_DTYPE_F32, vp(db), None, N, vp(dC), N,
+                           M, N, K, 0, stream(torch)))
+    torch.cuda.synchronize()
+    want = A.astype(np.float64) @ W.T.astype(np.float64) + bias
+    np.testing.assert_allclose(dC.cpu().numpy(), want, rtol=0, atol=1e-4)
+    del big
+    torch.cuda.empty_cache()
+
+
 @pytest.mark.parametrize("M,N,K,epi", [
     (4100, 1152, 384, 0),      # 128 x 128 tiles, 8 waves (row tail of 4)
     (8192, 384, 1536, 3),      # 8 waves, long K, no bias
@@ -343,6 +369,10 @@ def attention64(qkv, cu, H, nh):
     # at most 128 tokens: 64-key chunks, the second one prefetched
     (384, 12, [1, 63, 64, 65, 100, 127, 128]),
     (768, 12, [1, 65, 128]),
+    # BERT-base heads (head_dim 64) up to max_position_embeddings = 512
+    # (src/lib.rs:100, 655): four 128-key chunks, the last one partial
+    (768, 12, [384, 511, 512]),
+    (768, 12, [512, 0, 300, 1, 449]),
 ])
 def test_attention(env, H, nh, lengths):
     torch, eb, Nn, L = env
@@ -370,14 +400,20 @@ _SHORT_RAGGED = [int(x) for x in np.random.default_rng(7).integers(1, 129, 120)]
     (384, 12, [1, 2, 31, 32, 33, 127, 128, 0]),
     (384, 12, _SHORT_RAGGED),
     (768, 12, _SHORT_RAGGED[:60]),
+    # BERT-base heads (head_dim 64) up to max_position_embeddings = 512
+    # (src/lib.rs:100, 655)
+    (768, 12, [384, 511, 512]),
+    (768, 12, [512, 0, 300, 1, 449]),
 ])
 def test_attention_bf16(env, H, nh, lengths):
     """bf16 q / k / v and context: the float64 attention of the same bf16 values,
     within the bf16 rounding of the probabilities and of the result.  Batches
-    whose sequences all have at most 128 tokens take the persistent kernel
-    (sequence x head items walked by each workgroup, the next item's K / V
-    prefetched): with empty sequences, and with 1,440 and 720 items, more
-    than the grid's workgroups."""
+    whose sequences all have at most 128 tokens take the short-sequence kernel:
+    one workgroup per (head, sequence), Q, K and V loaded straight into LDS,
+    the scores waiting for Q and K only; the ragged cases (120 and 60
+    sequences of 1-128 tokens) and the ones with an empty sequence run that
+    path, the others the chunked kernel for longer sequences (128-key chunks
+    through registers, online softmax)."""
     torch, eb, Nn, L = env
     rng = np.random.default_rng(sum(lengths) + H + 1)
     T = sum(lengths)
