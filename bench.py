@@ -65,17 +65,29 @@ def few_fused(cfg, B: int, S: int, dtype: str) -> bool:
     return dtype != "bf16" and 0 < B * S <= 64 and H == 384 and H == 32 * nh
 
 
-def kernel_work(cfg, lengths, B: int, which: str, fused: bool = False):
+def kernel_work(cfg, lengths, B: int, which: str, fused: bool = False, dtype: str = "fp32"):
     """Algorithmic work of ONE launch of a kernel family: (amount, bound, unit).
 
     GEMMs: 2*T*N*K FLOPs over the T valid tokens.  Attention: 4*H*sum(l^2)
-    FLOPs (q.k^T and p.v at 2 FLOP per MAC).  Row kernels: the HBM bytes the
-    op must move at minimum (each operand read once, each result written once).
-    fused: the few-token layer's launches (few_fused).
+    FLOPs (q.k^T and p.v at 2 FLOP per MAC); with bf16 q / k / v (bf16 models)
+    the kernel is HBM-bound instead: q, k, v read and the context written once,
+    4*T*H*2 bytes.  Row kernels: the HBM bytes the op must move at minimum
+    (each operand read once, each result written once), in the activation
+    encoding of the model (bf16 models keep the GEMM outputs and the residual
+    stream in bf16).  fused: the few-token layer's launches (few_fused).
     """
     H, I = cfg.hidden_size, cfg.intermediate_size
     lengths = np.asarray(lengths, np.float64)
     T = float(lengths.sum())
+    if dtype == "bf16":
+        if which == "attention":
+            return 4.0 * T * H * 2, "hbm", "byte"
+        if which == "layernorm":      # bf16 product and residual read, bf16 residual written
+            return 3.0 * T * H * 2 + 3 * H * 4, "hbm", "byte"
+        if which == "embed":          # fp32 word / position rows in, bf16 row written
+            return T * (8 + 2 * H * 4 + H * 2) + 3 * H * 4, "hbm", "byte"
+        if which == "pool":           # the bf16 residual stream once, one fp32 vector per sequence
+            return T * H * 2 + B * H * 4 + (B + 1) * 4, "hbm", "byte"
     if fused and which == "attention":
         return 2.0 * T * H * H + 4.0 * H * float((lengths ** 2).sum()), "mfma", "flop"
     if fused and which == "gemm_out":
@@ -338,7 +350,7 @@ def config_leg(eb, torch, name: str, steps: int, warmup: int, graph_replay: bool
         if not launches:
             continue
         avg = prof_ms / launches
-        work, bound, wunit = kernel_work(cfg, lengths, B, fam, fused)
+        work, bound, wunit = kernel_work(cfg, lengths, B, fam, fused, dtype)
         if bound == "mfma":
             achieved, peak, punit = work / (avg * 1e-3) / 1e12, PEAK_TFLOPS[dtype], "TFLOP/s"
         else:
@@ -456,7 +468,7 @@ def main():
     tokens = int(mask.sum())
     avg_kernel_ms = prof_ms / max(launches, 1)
     fused = few_fused(cfg, B, S, dtype)
-    work, bound, wunit = kernel_work(cfg, lengths, B, args.profile_kernel, fused)
+    work, bound, wunit = kernel_work(cfg, lengths, B, args.profile_kernel, fused, dtype)
     if bound == "mfma":
         achieved, peak, punit = work / (avg_kernel_ms * 1e-3) / 1e12, PEAK_TFLOPS[dtype], "TFLOP/s"
     else:
@@ -528,7 +540,7 @@ def main():
         n, fms = model.profile_read()
         model.profile_enable("none")
         if n:
-            fwork, fbound, _ = kernel_work(cfg, lengths, B, fam, fused)
+            fwork, fbound, _ = kernel_work(cfg, lengths, B, fam, fused, dtype)
             favg = fms / n
             if fbound == "mfma":
                 fa, fp, fu = fwork / (favg * 1e-3) / 1e12, PEAK_TFLOPS[dtype], "TFLOP/s"
