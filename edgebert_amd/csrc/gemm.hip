@@ -277,7 +277,7 @@ __device__ __forceinline__ void split3_bf16(const v4f& x0, const v4f& x1, v8bf& 
 }
 
 template <bool BF16, bool OUT16, int BM, int BN, int BK, int WAVES_M, int WAVES_N, int NSTAGE, int EPI,
-          bool SPLIT6 = false>
+          bool SPLIT6 = false, bool MF16 = false>
 __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_persistent_kernel(GemmArgs p) {
     constexpr int ES = BF16 ? 2 : 4;              // bytes per element
     constexpr int EPC = 16 / ES;                  // elements per 16-byte chunk
@@ -290,6 +290,15 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_persistent_kernel
     constexpr int WM = BM / WAVES_M, WN = BN / WAVES_N;
     constexpr int FM = WM / 32, FN = WN / 32;
     static_assert(FM * 32 == WM && FN * 32 == WN, "wave tile must be whole 32x32 blocks");
+    // MF16 (bf16 operands): v_mfma_f32_16x16x32_bf16 on 16x16 blocks instead
+    // of v_mfma_f32_32x32x16_bf16 on 32x32 blocks.  The flops per cycle are
+    // the same, but these kernels are power-bound, and measured on MI355X with
+    // random operands a stream of the 16x16 form holds a higher clock under
+    // sustained load (1.95 against 1.76 GHz from registers; 1.85 against
+    // 1.64-1.71 GHz with a GEMM's LDS fragment reads beside them).
+    static_assert(!MF16 || (BF16 && !SPLIT6 && EPI != EPI_ADD_LN && BK == 64), "16x16x32 MFMAs: bf16, 64-deep k-tiles");
+    constexpr int FM16 = WM / 16, FN16 = WN / 16;
+    static_assert(!MF16 || FM16 % 2 == 0, "16x16 steps take half of the wave tile's row blocks each");
     constexpr int CPR = BK / EPC;                 // 16-byte chunks per tile row
     constexpr int KS = CPR / 2;                   // k-slices (two chunks: one per lane half)
     constexpr int RW = CPR * 4;                   // words per tile row
@@ -429,11 +438,19 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_persistent_kernel
 
     const int sw = chunk_swizzle16<CPR>(l32);
     const int a_row = (wm * WM + l32) * RW, w_row = BM * RW + (wn * WN + l32) * RW;
+    // 16x16x32 blocks: lane (r16, q16) gives row r16 of a block at k-chunk
+    // q16 of the 32-deep slice (16 bytes; A and W use the same map), and holds
+    // D[4 q16 + e][r16] of D = W.A^T, i.e. C row r16, columns 4 q16 .. +3.
+    // Block rows are multiples of 16, so a block's swizzle is that of r16.
+    const int r16 = lane & 15, q16 = lane >> 4;
+    const int sw16 = chunk_swizzle16<CPR>(r16);
+    const int a_row16 = (wm * WM + r16) * RW, w_row16 = BM * RW + (wn * WN + r16) * RW;
     // Epilogue lane map: pass qq of block row i covers wave-tile rows
     // i*32 + qq*RPP + lane / C4, columns 4 * (lane % C4) .. +3.
     const int e_r = lane / C4, e_c = 4 * (lane % C4);
 
     v16f acc[FM][FN];
+    v4f acc16[FM16][FN16];
 
     // EPI_ADD_LN: the tile spans whole rows (one tile column), so the workgroup
     // holds every value of its rows.  Lane (l32, half) of wave (wm, wn) holds,
@@ -726,8 +743,87 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_persistent_kernel
         }
     };
 
+    // Packed bf16 epilogue of the 16x16x32 blocks: acc16[i][j][e] is C at
+    // wave-tile row 16 i + r16, column 16 j + 4 q16 + e.  Two row blocks (32
+    // rows) at a time go through the wave's LDS slot as in epilogue_packed.
+    auto epilogue_packed16 = [&](int t, const float* cs_base) __attribute__((always_inline)) {
+        const int u = wg + t * G, split = u / ntiles, tile = u - split * ntiles;
+        uint16_t* const Cs = reinterpret_cast<uint16_t*>(p.C) + (int64_t)split * p.split_stride;
+        const int m0 = (tile / ntiles_n) * BM, n0 = (tile - (tile / ntiles_n) * ntiles_n) * BN;
+        const float* bslot = smem + NSTAGE * STAGE + ((t & 1) * NW + wave) * BIAS_SLOT;
+        char* cw = reinterpret_cast<char*>(const_cast<float*>(cs_base) + wave * (16 * WN));
+        constexpr int CPW = WN / 8;               // 16-byte chunks per wave-tile row
+        constexpr int NPASS = 32 * CPW / 64;
+        const bool wide = (p.ldc & 7) == 0;       // rows 16-byte aligned
+#pragma unroll
+        for (int ip = 0; ip < FM16 / 2; ++ip) {
+#pragma unroll
+            for (int ii = 0; ii < 2; ++ii)
+#pragma unroll
+                for (int j = 0; j < FN16; ++j) {
+                    const v4f a = acc16[2 * ip + ii][j];
+                    float4 v = make_float4(a[0], a[1], a[2], a[3]);
+                    if (HAS_BIAS) {
+                        const float4 b4 = *reinterpret_cast<const float4*>(bslot + j * 16 + 4 * q16);
+                        v.x += b4.x; v.y += b4.y; v.z += b4.z; v.w += b4.w;
+                    }
+                    if constexpr (EPI == EPI_BIAS_GELU) {
+                        v.x = gelu_tanh_fast(v.x); v.y = gelu_tanh_fast(v.y);
+                        v.z = gelu_tanh_fast(v.z); v.w = gelu_tanh_fast(v.w);
+                    }
+                    const uint2 h = make_uint2(pack_bf16x2(v.x, v.y), pack_bf16x2(v.z, v.w));
+                    const int r = 16 * ii + r16;
+                    *reinterpret_cast<uint2*>(cw + r * (2 * WN) + (((2 * j + (q16 >> 1)) ^ (r & 7)) << 4) +
+                                              8 * (q16 & 1)) = h;
+                }
+#pragma unroll
+            for (int ps = 0; ps < NPASS; ++ps) {
+                const int q = ps * 64 + lane, r = q / CPW, c = q - r * CPW;
+                const uint4 d = *reinterpret_cast<const uint4*>(cw + r * (2 * WN) + ((c ^ (r & 7)) << 4));
+                const int grow = m0 + wm * WM + ip * 32 + r, gcol = n0 + wn * WN + 8 * c;
+                if (grow < M && gcol < N) {   // N % 4 == 0: the chunk's first 4 columns are in
+                    uint16_t* dst = Cs + (int64_t)grow * p.ldc + gcol;
+                    if (wide && gcol + 8 <= N) {
+                        typedef unsigned int u4v __attribute__((ext_vector_type(4)));
+                        __builtin_nontemporal_store(u4v{d.x, d.y, d.z, d.w}, reinterpret_cast<u4v*>(dst));
+                    } else {
+                        *reinterpret_cast<uint2*>(dst) = make_uint2(d.x, d.y);
+                        if (gcol + 8 <= N) *reinterpret_cast<uint2*>(dst + 4) = make_uint2(d.z, d.w);
+                    }
+                }
+            }
+        }
+    };
+    // fp32 output of the 16x16x32 blocks (the op-level bf16 GEMM with an fp32
+    // C): each lane's four consecutive columns of a row as one float4 store.
+    auto epilogue_direct16 = [&](int t) __attribute__((always_inline)) {
+        const int u = wg + t * G, split = u / ntiles, tile = u - split * ntiles;
+        float* const Cs = p.C + (int64_t)split * p.split_stride;
+        const int m0 = (tile / ntiles_n) * BM, n0 = (tile - (tile / ntiles_n) * ntiles_n) * BN;
+        const float* bslot = smem + NSTAGE * STAGE + ((t & 1) * NW + wave) * BIAS_SLOT;
+#pragma unroll
+        for (int i = 0; i < FM16; ++i)
+#pragma unroll
+            for (int j = 0; j < FN16; ++j) {
+                const v4f a = acc16[i][j];
+                float4 v = make_float4(a[0], a[1], a[2], a[3]);
+                if (HAS_BIAS) {
+                    const float4 b4 = *reinterpret_cast<const float4*>(bslot + j * 16 + 4 * q16);
+                    v.x += b4.x; v.y += b4.y; v.z += b4.z; v.w += b4.w;
+                }
+                if constexpr (EPI == EPI_BIAS_GELU) {
+                    v.x = gelu_tanh_fast(v.x); v.y = gelu_tanh_fast(v.y);
+                    v.z = gelu_tanh_fast(v.z); v.w = gelu_tanh_fast(v.w);
+                }
+                const int grow = m0 + wm * WM + 16 * i + r16, gcol = n0 + wn * WN + 16 * j + 4 * q16;
+                if (grow < M && gcol < N) *reinterpret_cast<float4*>(Cs + (int64_t)grow * p.ldc + gcol) = v;
+            }
+    };
+
     auto finish_tile = [&](int t, float* stage) __attribute__((always_inline)) {
         if constexpr (LN) epilogue_ln(t, stage);
+        else if constexpr (MF16 && OUT16) epilogue_packed16(t, stage);
+        else if constexpr (MF16) epilogue_direct16(t);
         else if constexpr (PACKED) epilogue_packed(t, stage);
         else if constexpr (FLAT) epilogue_flat(t, stage);
         else epilogue_tile(t, stage);
@@ -772,11 +868,41 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_persistent_kernel
     // behind a branch on the k-tile index: accumulators merged from two paths
     // cost the register allocator a second copy of them.
     constexpr bool DEFER = PREF && KS % 2 == 0 && !SPLIT6;
+    // MF16: a 64-deep k-tile runs as four steps of 16 MFMAs (256 cycles, as
+    // one 16-deep slice of the 32x32 form): step s4 = 2 sl + h multiplies the
+    // A blocks of half h of the wave tile's rows by the W blocks of 32-deep
+    // slice sl.  A step's A fragments are read during the previous step (two
+    // sets); a slice's W fragments with its first step's A fragments (two
+    // sets).  So the fragment registers stay those of the 32x32 form's two
+    // sets (plus one W set), within two waves per SIMD.
+    v4f a16b[2][FM16 / 2], w16b[2][FN16];
+    auto mfma16 = [&](int s4) __attribute__((always_inline)) {
+        const int sl = s4 >> 1, h = s4 & 1;
+#pragma unroll
+        for (int i = 0; i < FM16 / 2; ++i)
+#pragma unroll
+            for (int j = 0; j < FN16; ++j)
+                acc16[h * (FM16 / 2) + i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                    __builtin_bit_cast(v8bf, w16b[sl & 1][j]), __builtin_bit_cast(v8bf, a16b[s4 & 1][i]),
+                    acc16[h * (FM16 / 2) + i][j], 0, 0, 0);
+    };
+    // The MFMAs deferred past the next k-tile's barrier: the last slice (or step).
+    auto last_step = [&]() __attribute__((always_inline)) {
+        if constexpr (MF16) mfma16(KS - 1);
+        else mfma_slice(1);
+    };
     if constexpr (DEFER) {
+        if constexpr (MF16) {
 #pragma unroll
-        for (int i = 0; i < FM; ++i) afb[1][i] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+            for (int i = 0; i < FM16 / 2; ++i) a16b[1][i] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-        for (int j = 0; j < FN; ++j) wfb[1][j] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+            for (int j = 0; j < FN16; ++j) w16b[1][j] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+        } else {
+#pragma unroll
+            for (int i = 0; i < FM; ++i) afb[1][i] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int j = 0; j < FN; ++j) wfb[1][j] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+        }
     }
 
     int it = 0;
@@ -834,6 +960,28 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_persistent_kernel
                     }
                 }
             }
+        } else if constexpr (MF16) {
+            static_assert(KS == 4, "four steps per 64-deep k-tile");
+            auto rd16 = [&](int s4, int b) __attribute__((always_inline)) {
+                const int sl = s4 >> 1, h = s4 & 1;
+                const int ko = 4 * ((4 * sl + q16) ^ sw16);
+#pragma unroll
+                for (int i = 0; i < FM16 / 2; ++i)
+                    a16b[b][i] = *reinterpret_cast<const v4f*>(st + a_row16 + (h * (FM16 / 2) + i) * 16 * RW + ko);
+                if (h == 0) {
+#pragma unroll
+                    for (int j = 0; j < FN16; ++j)
+                        w16b[sl & 1][j] = *reinterpret_cast<const v4f*>(st + w_row16 + j * 16 * RW + ko);
+                }
+            };
+            rd16(0, 0);
+            if constexpr (DEFER && !decltype(first)::value) mfma16(KS - 1);   // k-tile it - 1's last step
+#pragma unroll
+            for (int s4 = 0; s4 < KS; ++s4) {
+                if (refill && s4 < NPART) issue_part(s4);
+                if (s4 + 1 < KS) rd16(s4 + 1, (s4 + 1) & 1);
+                if (!(DEFER && s4 == KS - 1)) mfma16(s4);
+            }
         } else {
             if (PREF) rd(0, 0);
             if constexpr (DEFER && !decltype(first)::value) mfma_slice(1);   // k-tile it - 1's last slice
@@ -853,17 +1001,24 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_persistent_kernel
         if (nit < total) issue();
     for (int t = 0; t < my_tiles; ++t) {
         enter_ktile();
-        if constexpr (DEFER && !LN) mfma_slice(1);   // the previous tile's last slice (zeros at t = 0)
+        if constexpr (DEFER && !LN) last_step();   // the previous tile's last slice (zeros at t = 0)
         if (!LN && t > 0) {
             finish_tile(t - 1, smem + ((it - 1) % NSTAGE) * STAGE);
             lds_barrier();  // the stage is refilled by the loads below
         }
+        if constexpr (MF16) {
 #pragma unroll
-        for (int i = 0; i < FM; ++i)
+            for (int i = 0; i < FM16; ++i)
 #pragma unroll
-            for (int j = 0; j < FN; ++j)
+                for (int j = 0; j < FN16; ++j) acc16[i][j] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+        } else {
 #pragma unroll
-                for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+            for (int i = 0; i < FM; ++i)
+#pragma unroll
+                for (int j = 0; j < FN; ++j)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+        }
         run_ktile(std::true_type{});
         ++it;
         for (int kt = 1; kt < nk; ++kt, ++it) {
@@ -880,7 +1035,7 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_persistent_kernel
         }
     }
     if constexpr (!LN) {
-        if constexpr (DEFER) mfma_slice(1);
+        if constexpr (DEFER) last_step();
         lds_barrier();  // every wave is done with the last k-tile's stage
         finish_tile(my_tiles - 1, smem + ((it - 1) % NSTAGE) * STAGE);
     }
@@ -1188,7 +1343,8 @@ int device_cu_count() {
 
 static int cu_count() { return device_cu_count(); }
 
-template <int BM, int BN, int BK, int WAVES_M, int WAVES_N, int NSTAGE, bool BF16, bool OUT16, bool SPLIT6>
+template <int BM, int BN, int BK, int WAVES_M, int WAVES_N, int NSTAGE, bool BF16, bool OUT16, bool SPLIT6,
+          bool MF16 = BF16 && !SPLIT6>
 static hipError_t launch_persistent_kernel(const GemmArgs& a, int epi, hipStream_t s, int wg_per_cu);
 
 template <int BM, int BN, int BK, int WAVES_M, int WAVES_N, int NSTAGE, bool BF16 = false, bool OUT16 = false>
@@ -1198,7 +1354,8 @@ static hipError_t launch_persistent(const GemmArgs& a, int epi, hipStream_t s, i
     return launch_persistent_kernel<BM, BN, BK, WAVES_M, WAVES_N, NSTAGE, BF16, OUT16, false>(a, epi, s, wg_per_cu);
 }
 
-template <int BM, int BN, int BK, int WAVES_M, int WAVES_N, int NSTAGE, bool BF16, bool OUT16, bool SPLIT6>
+template <int BM, int BN, int BK, int WAVES_M, int WAVES_N, int NSTAGE, bool BF16, bool OUT16, bool SPLIT6,
+          bool MF16>
 static hipError_t launch_persistent_kernel(const GemmArgs& a, int epi, hipStream_t s, int wg_per_cu) {
     // One work item per tile and k-split.
     const int64_t items = (int64_t)((a.M_max + BM - 1) / BM) * ((a.N + BN - 1) / BN) * (a.splits > 1 ? a.splits : 1);
@@ -1207,13 +1364,13 @@ static hipError_t launch_persistent_kernel(const GemmArgs& a, int epi, hipStream
     const dim3 block(64 * WAVES_M * WAVES_N);
     switch (epi) {
         case EPI_BIAS:
-            hipLaunchKernelGGL((gemm_persistent_kernel<BF16, OUT16, BM, BN, BK, WAVES_M, WAVES_N, NSTAGE, EPI_BIAS, SPLIT6>), dim3(grid), block, 0, s, a);
+            hipLaunchKernelGGL((gemm_persistent_kernel<BF16, OUT16, BM, BN, BK, WAVES_M, WAVES_N, NSTAGE, EPI_BIAS, SPLIT6, MF16>), dim3(grid), block, 0, s, a);
             break;
         case EPI_BIAS_GELU:
-            hipLaunchKernelGGL((gemm_persistent_kernel<BF16, OUT16, BM, BN, BK, WAVES_M, WAVES_N, NSTAGE, EPI_BIAS_GELU, SPLIT6>), dim3(grid), block, 0, s, a);
+            hipLaunchKernelGGL((gemm_persistent_kernel<BF16, OUT16, BM, BN, BK, WAVES_M, WAVES_N, NSTAGE, EPI_BIAS_GELU, SPLIT6, MF16>), dim3(grid), block, 0, s, a);
             break;
         case EPI_NONE:
-            hipLaunchKernelGGL((gemm_persistent_kernel<BF16, OUT16, BM, BN, BK, WAVES_M, WAVES_N, NSTAGE, EPI_NONE, SPLIT6>), dim3(grid), block, 0, s, a);
+            hipLaunchKernelGGL((gemm_persistent_kernel<BF16, OUT16, BM, BN, BK, WAVES_M, WAVES_N, NSTAGE, EPI_NONE, SPLIT6, MF16>), dim3(grid), block, 0, s, a);
             break;
         default:
             return hipErrorInvalidValue;
