@@ -296,7 +296,8 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_persistent_kernel
     // random operands a stream of the 16x16 form holds a higher clock under
     // sustained load (1.95 against 1.76 GHz from registers; 1.85 against
     // 1.64-1.71 GHz with a GEMM's LDS fragment reads beside them).
-    static_assert(!MF16 || (BF16 && !SPLIT6 && EPI != EPI_ADD_LN && BK == 64), "16x16x32 MFMAs: bf16, 64-deep k-tiles");
+    static_assert(!MF16 || (BF16 && !SPLIT6 && EPI != EPI_ADD_LN && (BK == 64 || BK == 32)),
+                  "16x16x32 MFMAs: bf16, 32- or 64-deep k-tiles");
     constexpr int FM16 = WM / 16, FN16 = WN / 16;
     static_assert(!MF16 || FM16 % 2 == 0, "16x16 steps take half of the wave tile's row blocks each");
     constexpr int CPR = BK / EPC;                 // 16-byte chunks per tile row
@@ -868,10 +869,10 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_persistent_kernel
     // behind a branch on the k-tile index: accumulators merged from two paths
     // cost the register allocator a second copy of them.
     constexpr bool DEFER = PREF && KS % 2 == 0 && !SPLIT6;
-    // MF16: a 64-deep k-tile runs as four steps of 16 MFMAs (256 cycles, as
-    // one 16-deep slice of the 32x32 form): step s4 = 2 sl + h multiplies the
-    // A blocks of half h of the wave tile's rows by the W blocks of 32-deep
-    // slice sl.  A step's A fragments are read during the previous step (two
+    // MF16: a k-tile runs as steps of 16 MFMAs (256 cycles, as one 16-deep
+    // slice of the 32x32 form), two per 32-deep slice: step s4 = 2 sl + h
+    // multiplies the A blocks of half h of the wave tile's rows by the W
+    // blocks of slice sl.  A step's A fragments are read during the previous step (two
     // sets); a slice's W fragments with its first step's A fragments (two
     // sets).  So the fragment registers stay those of the 32x32 form's two
     // sets (plus one W set), within two waves per SIMD.
@@ -961,7 +962,7 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_persistent_kernel
                 }
             }
         } else if constexpr (MF16) {
-            static_assert(KS == 4, "four steps per 64-deep k-tile");
+            static_assert(KS == 2 * (BK / 32), "two steps per 32-deep slice");
             auto rd16 = [&](int s4, int b) __attribute__((always_inline)) {
                 const int sl = s4 >> 1, h = s4 & 1;
                 const int ko = 4 * ((4 * sl + q16) ^ sw16);
@@ -1039,6 +1040,271 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_persistent_kernel
         lds_barrier();  // every wave is done with the last k-tile's stage
         finish_tile(my_tiles - 1, smem + ((it - 1) % NSTAGE) * STAGE);
     }
+}
+
+// ---------------------------------------------------------------------------
+// bf16 products with bf16 outputs (every Linear of a bf16 model): 256 x 256
+// C tiles, 64-deep k-tiles, 8 waves of 128 x 64 on v_mfma_f32_16x16x32_bf16,
+// persistent over a strided list of tiles (one workgroup per CU).
+//
+// Measured on MI355X, the 2-stage kernel above loses its time at three places
+// besides the MFMAs: waiting for the k-tile's loads (the A panels stream from
+// HBM, and one k-tile of lookahead leaves their latency exposed: 9-15% of a
+// wave's cycles, up to 37% at a higher clock), the epilogue's stores (a CU
+// issues stores at ~25 B/clk, so a 128 KB output tile takes ~5k cycles, and
+// the next k-tile's loads queue behind them in the in-order vmcnt), and the
+// GELU.  This kernel:
+//  * keeps A k-tiles in a ring of three LDS stages (two k-tiles in flight
+//    ahead) and W k-tiles, which the L2 / last-level cache holds, in a ring of
+//    two: 3 x 32 KB + 2 x 32 KB, the whole 160 KB;
+//  * starts each tile's accumulators at its bias (the bias row segment rides
+//    into the freed A stage with the tile's first k-tile), so the epilogue
+//    adds nothing and needs no LDS of its own beyond that stage;
+//  * issues the next W k-tile before the epilogue's stores and counts every
+//    vector memory instruction it issues (the stores are buffer stores whose
+//    rows past M or columns past N get an offset past the descriptor's end,
+//    so every lane issues every store and the count is exact).  The next
+//    k-tile then waits for its W without waiting for the stores, which drain
+//    during its MFMAs and are only waited for a k-tile later.
+// Load order per k-tile j: W(j + 1), then A(j + 2) (at a tile's first k-tile:
+// the bias, W(j + 1), the stores, then A(j + 2)).  Waiting for W(j) covers
+// A(j) too, which was issued before it.
+// ---------------------------------------------------------------------------
+template <int EPI>
+__global__ __launch_bounds__(512) void gemm_bf16_ring_kernel(GemmArgs p) {
+    constexpr int BM = 256, BN = 256, BK = 64, NT = 512, WAVES_N = 4;
+    constexpr int WM = 128, WN = 64, FM16 = WM / 16, FN16 = WN / 16, HALF = FM16 / 2;
+    constexpr int CPR = BK / 8, RW = 4 * CPR;     // 16-byte chunks / 4-byte words per tile row
+    constexpr int SA = BM * RW, SW = BN * RW;     // words per A / W stage
+    constexpr int LA = BM * CPR / NT, LW = BN * CPR / NT;
+    static_assert(LA == LW, "A and W tiles share the lane load pattern");
+    constexpr int EROWS = 16;                     // C rows per epilogue pass (one row block)
+    constexpr int CPW = WN / 8;                   // 16-byte chunks per wave-tile row
+    constexpr int ST_PASS = EROWS * CPW / 64;     // stores per lane per pass
+    constexpr int N_ST = FM16 * ST_PASS;          // stores per lane per tile
+    constexpr int STAGE_WORDS = 512, BIAS_WORDS = 256;   // per wave, within the freed A stage
+    static_assert(8 * STAGE_WORDS + 8 * BIAS_WORDS <= SA, "epilogue staging and bias fit one A stage");
+    constexpr bool HAS_BIAS = EPI != EPI_NONE;
+    __shared__ __attribute__((aligned(16))) float smem[3 * SA + 2 * SW];
+    float* const sA = smem;
+    float* const sW = smem + 3 * SA;
+
+    const int M = p.M_dev ? *p.M_dev : p.M_max;
+    const int N = p.N;
+    const int ntiles_n = (N + BN - 1) / BN;
+    const int ntiles = ((M + BM - 1) / BM) * ntiles_n;
+    const int nk = p.K / BK;
+    const int G = gridDim.x;
+    const int wg = (G & 7) == 0 ? (blockIdx.x & 7) * (G >> 3) + (blockIdx.x >> 3) : blockIdx.x;
+    const int my_tiles = wg < ntiles ? (ntiles - wg + G - 1) / G : 0;
+    const int total = my_tiles * nk;
+    if (total == 0) return;  // uniform over the workgroup
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wm = wave / WAVES_N, wn = wave % WAVES_N;
+    const char* __restrict__ A = static_cast<const char*>(p.A);
+    const char* __restrict__ W = static_cast<const char*>(p.W);
+
+    // Lane share of each k-tile load (A and W alike): LDS chunk i*NT + tid,
+    // tile row r, holding global chunk (position ^ swizzle(r)).
+    int l_r[LA], l_c[LA];
+#pragma unroll
+    for (int i = 0; i < LA; ++i) {
+        const int P = i * NT + tid;
+        l_r[i] = P / CPR;
+        l_c[i] = 8 * ((P % CPR) ^ chunk_swizzle16<CPR>(P / CPR));   // elements
+    }
+    // Load cursors: the next A / W k-tile to load (global iteration index),
+    // its panel base (wave-uniform) and this lane's 32-bit byte offsets.
+    int ia = 0, iw = 0;
+    uint64_t abase = 0, wbase = 0;
+    uint32_t aoff[LA], woff[LA];
+    auto a_seek = [&](int x) __attribute__((always_inline)) {
+        const int ti = x / nk, kt = x - ti * nk;
+        const int m0 = ((wg + ti * G) / ntiles_n) * BM;
+#pragma unroll
+        for (int i = 0; i < LA; ++i) aoff[i] = (uint32_t)(((min(m0 + l_r[i], M - 1) - m0) * p.lda + l_c[i]) * 2);
+        abase = uniform_u64(A + ((int64_t)m0 * p.lda + (int64_t)kt * BK) * 2);
+    };
+    auto w_seek = [&](int x) __attribute__((always_inline)) {
+        const int ti = x / nk, kt = x - ti * nk;
+        const int n0 = ((wg + ti * G) % ntiles_n) * BN;
+#pragma unroll
+        for (int i = 0; i < LA; ++i) woff[i] = (uint32_t)(((min(n0 + l_r[i], N - 1) - n0) * p.ldw + l_c[i]) * 2);
+        wbase = uniform_u64(W + ((int64_t)n0 * p.ldw + (int64_t)kt * BK) * 2);
+    };
+    // Vector memory instructions this wave has issued (loads, bias, stores)
+    // and the count right after the last W k-tile / bias load.
+    int vm = 0, w_mark = 0, b_mark = 0;
+    auto issue_a = [&]() __attribute__((always_inline)) {
+        if (ia >= total) return;
+        float* st = sA + (ia % 3) * SA;
+#pragma unroll
+        for (int i = 0; i < LA; ++i) load_lds16_sbase(abase, aoff[i], st + (i * NT + wave * 64) * 4);
+        vm += LA;
+        if (++ia < total) {
+            if (ia % nk == 0) a_seek(ia);
+            else abase += BK * 2;
+        }
+    };
+    auto issue_w = [&]() __attribute__((always_inline)) {
+        if (iw >= total) return;
+        float* st = sW + (iw & 1) * SW;
+#pragma unroll
+        for (int i = 0; i < LA; ++i) load_lds16_sbase(wbase, woff[i], st + (i * NT + wave * 64) * 4);
+        vm += LA;
+        w_mark = vm;
+        if (++iw < total) {
+            if (iw % nk == 0) w_seek(iw);
+            else wbase += BK * 2;
+        }
+    };
+    // Bias of local tile t, this wave's 64 columns (lanes past them load
+    // clamped copies), into the wave's slot of A stage `st`.
+    auto issue_bias = [&](int t, float* st) __attribute__((always_inline)) {
+        const int n0 = ((wg + t * G) % ntiles_n) * BN;
+        load_lds16_async(p.bias + min(n0 + wn * WN + 4 * lane, N - 4), st + 8 * STAGE_WORDS + wave * BIAS_WORDS);
+        vm += 1;
+        b_mark = vm;
+    };
+
+    const int r16 = lane & 15, q16 = lane >> 4;
+    const int sw16 = chunk_swizzle16<CPR>(r16);
+    const int a_row16 = (wm * WM + r16) * RW, w_row16 = (wn * WN + r16) * RW;
+    v4f acc16[FM16][FN16];
+    v4f a16b[2][HALF], w16b[2][FN16];
+    // Step s4 = 2 sl + h of a k-tile: the A blocks of row half h against the
+    // W blocks of 32-deep slice sl (fragments read a step ahead, two sets).
+    auto mfma16 = [&](int s4) __attribute__((always_inline)) {
+        const int sl = s4 >> 1, h = s4 & 1;
+#pragma unroll
+        for (int i = 0; i < HALF; ++i)
+#pragma unroll
+            for (int j = 0; j < FN16; ++j)
+                acc16[h * HALF + i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                    __builtin_bit_cast(v8bf, w16b[sl & 1][j]), __builtin_bit_cast(v8bf, a16b[s4 & 1][i]),
+                    acc16[h * HALF + i][j], 0, 0, 0);
+    };
+    auto rd16 = [&](const float* stA, const float* stW, int s4, int b) __attribute__((always_inline)) {
+        const int sl = s4 >> 1, h = s4 & 1;
+        const int ko = 4 * ((4 * sl + q16) ^ sw16);
+#pragma unroll
+        for (int i = 0; i < HALF; ++i)
+            a16b[b][i] = *reinterpret_cast<const v4f*>(stA + a_row16 + (h * HALF + i) * 16 * RW + ko);
+        if (h == 0) {
+#pragma unroll
+            for (int j = 0; j < FN16; ++j)
+                w16b[sl & 1][j] = *reinterpret_cast<const v4f*>(stW + w_row16 + j * 16 * RW + ko);
+        }
+    };
+    // The MFMAs of global k-tile j; the last step is left for after the next
+    // barrier.  Away from a tile's first k-tile the previous k-tile's last
+    // step runs first and the loads W(j + 1), A(j + 2) go out with steps 0, 1.
+    auto run_ktile = [&](int j, bool first) __attribute__((always_inline)) {
+        const float* stA = sA + (j % 3) * SA;
+        const float* stW = sW + (j & 1) * SW;
+        rd16(stA, stW, 0, 0);
+        if (!first) mfma16(3);
+#pragma unroll
+        for (int s4 = 0; s4 < 3; ++s4) {
+            if (!first && s4 == 0) issue_w();
+            if (!first && s4 == 1) issue_a();
+            rd16(stA, stW, s4 + 1, (s4 + 1) & 1);
+            mfma16(s4);
+        }
+    };
+
+    // Epilogue of local tile t (GELU or nothing: the bias is in the
+    // accumulators), one 16-row block at a time through the wave's 2 KB of
+    // the freed A stage `st`, then 16-byte buffer stores of whole row chunks.
+    auto epilogue = [&](int t, float* st) __attribute__((always_inline)) {
+        const int u = wg + t * G;
+        const int m0 = (u / ntiles_n) * BM, n0 = (u % ntiles_n) * BN;
+        const int valid = min(M - m0, BM);
+        const __amdgpu_buffer_rsrc_t cr = __builtin_amdgcn_make_buffer_rsrc(
+            reinterpret_cast<uint16_t*>(p.C) + (int64_t)m0 * p.ldc, (short)0,
+            (int)(uint32_t)((uint64_t)valid * p.ldc * 2), BUFFER_RSRC_WORD3);
+        // Lane-derived values opaque here: computed at the stores, not held
+        // across the k-loop (the last tile's epilogue follows it).
+        int el = lane, er = r16, eq = q16, ew = wave;
+        asm volatile("" : "+v"(el), "+v"(er), "+v"(eq), "+v"(ew));
+        char* cw = reinterpret_cast<char*>(st + ew * STAGE_WORDS);
+#pragma unroll
+        for (int i = 0; i < FM16; ++i) {
+#pragma unroll
+            for (int j = 0; j < FN16; ++j) {
+                const v4f a = acc16[i][j];
+                float4 v = make_float4(a[0], a[1], a[2], a[3]);
+                if constexpr (EPI == EPI_BIAS_GELU) {
+                    v.x = gelu_tanh_fast(v.x); v.y = gelu_tanh_fast(v.y);
+                    v.z = gelu_tanh_fast(v.z); v.w = gelu_tanh_fast(v.w);
+                }
+                const uint2 h = make_uint2(pack_bf16x2(v.x, v.y), pack_bf16x2(v.z, v.w));
+                *reinterpret_cast<uint2*>(cw + er * (2 * WN) + (((2 * j + (eq >> 1)) ^ (er & 7)) << 4) +
+                                          8 * (eq & 1)) = h;
+            }
+#pragma unroll
+            for (int ps = 0; ps < ST_PASS; ++ps) {
+                const int q = ps * 64 + el, r = q / CPW, c = q - r * CPW;
+                const uint4 d = *reinterpret_cast<const uint4*>(cw + r * (2 * WN) + ((c ^ (r & 7)) << 4));
+                const int row = (ew / WAVES_N) * WM + i * EROWS + r, col = n0 + (ew % WAVES_N) * WN + 8 * c;
+                const uint32_t off = row < valid && col < N ? (uint32_t)((row * p.ldc + col) * 2) : 0xFFFFFFF0u;
+                typedef unsigned int u4v __attribute__((ext_vector_type(4)));
+                __builtin_amdgcn_raw_buffer_store_b128(u4v{d.x, d.y, d.z, d.w}, cr, off, 0, 2 /* nt */);
+            }
+        }
+        vm += N_ST;
+    };
+
+    // Prologue: bias(0) into the stage A(2) will take, A(0), W(0), A(1).
+    a_seek(0);
+    w_seek(0);
+    if (HAS_BIAS) issue_bias(0, sA + 2 * SA);
+    issue_a();
+    issue_w();
+    issue_a();
+    int j = 0;
+    for (int t = 0; t < my_tiles; ++t) {
+        // First k-tile of tile t: W(j) (and so A(j) and the bias) landed.
+        wait_vmcnt(vm - w_mark);
+        lds_barrier();
+        float* freed = sA + ((j + 2) % 3) * SA;   // A stage of k-tile j - 1
+        if (t > 0) {
+            if (HAS_BIAS) issue_bias(t, freed);
+            mfma16(3);                 // tile t - 1's last step
+        }
+        issue_w();                     // W(j + 1), before the stores
+        if (t > 0) {
+            epilogue(t - 1, freed);
+            if (HAS_BIAS) wait_vmcnt(vm - b_mark);
+        }
+        if constexpr (HAS_BIAS) {
+            const float* bs = freed + 8 * STAGE_WORDS + wave * BIAS_WORDS;
+#pragma unroll
+            for (int jj = 0; jj < FN16; ++jj) {
+                const v4f b4 = *reinterpret_cast<const v4f*>(bs + 16 * jj + 4 * q16);
+#pragma unroll
+                for (int i = 0; i < FM16; ++i) acc16[i][jj] = b4;
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < FM16; ++i)
+#pragma unroll
+                for (int jj = 0; jj < FN16; ++jj) acc16[i][jj] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+        }
+        lds_barrier();                 // the freed stage is refilled next
+        issue_a();                     // A(j + 2)
+        run_ktile(j, true);
+        ++j;
+        for (int kt = 1; kt < nk; ++kt, ++j) {
+            wait_vmcnt(vm - w_mark);
+            lds_barrier();
+            run_ktile(j, false);
+        }
+    }
+    mfma16(3);
+    lds_barrier();
+    epilogue(my_tiles - 1, sA + ((j + 2) % 3) * SA);
 }
 
 // ---------------------------------------------------------------------------
@@ -1505,6 +1771,18 @@ hipError_t launch_gemm_bf16_act(const GemmArgs& a, int epi, bool c_bf16, hipStre
                     a.ldc % 4 == 0 && a.N % 4 == 0 && a.K % 64 == 0 && a.K > 0 &&
                     gemm_offsets_fit32(a.lda, a.ldw, 2);
     if (!ok) return hipErrorInvalidValue;
+    if (c_bf16 && a.N % 8 == 0 && a.ldc % 8 == 0 && (epi == EPI_NONE || aligned16(a.bias))) {
+        const int64_t tiles = (int64_t)((a.M_max + 255) / 256) * ((a.N + 255) / 256);
+        if (tiles == 0) return hipSuccess;
+        const dim3 grid((unsigned)std::min<int64_t>(tiles, cu_count())), block(512);
+        switch (epi) {
+            case EPI_BIAS: hipLaunchKernelGGL(gemm_bf16_ring_kernel<EPI_BIAS>, grid, block, 0, s, a); break;
+            case EPI_BIAS_GELU: hipLaunchKernelGGL(gemm_bf16_ring_kernel<EPI_BIAS_GELU>, grid, block, 0, s, a); break;
+            case EPI_NONE: hipLaunchKernelGGL(gemm_bf16_ring_kernel<EPI_NONE>, grid, block, 0, s, a); break;
+            default: return hipErrorInvalidValue;
+        }
+        return hipGetLastError();
+    }
     if (c_bf16) return launch_persistent<256, 256, 64, 2, 4, 2, true, true>(a, epi, s, 1);
     return launch_persistent<256, 256, 64, 2, 4, 2, true, false>(a, epi, s, 1);
 }
