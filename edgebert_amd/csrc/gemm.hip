@@ -912,7 +912,10 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_persistent_kernel
     auto enter_ktile = [&]() __attribute__((always_inline)) {
         int after = 0;
         for (int j = it + 1; j < nit; ++j) after += n_issued(j);
-        wait_vmcnt(after);
+        if constexpr (D == 1)   // one k-tile ahead: after is 0, NL or NL + 1
+            wait_vmcnt_of<NL + (HAS_BIAS ? 1 : 0), NL>(after);
+        else
+            wait_vmcnt(after);
         lds_barrier();
     };
     // The MFMAs of k-tile `it` (its loads have landed), and the loads of a
@@ -1264,9 +1267,13 @@ __global__ __launch_bounds__(512) void gemm_bf16_ring_kernel(GemmArgs p) {
     issue_w();
     issue_a();
     int j = 0;
+    // Counts that occur after W(j): A(j + 1), and the stores and A(j + 1)
+    // when j - 1 was a tile's first k-tile; after the bias: W(j + 1) and the
+    // stores.
+    auto wait_after = [&](int n) __attribute__((always_inline)) { wait_vmcnt_of<N_ST + LA, N_ST, LA>(n); };
     for (int t = 0; t < my_tiles; ++t) {
         // First k-tile of tile t: W(j) (and so A(j) and the bias) landed.
-        wait_vmcnt(vm - w_mark);
+        wait_after(vm - w_mark);
         lds_barrier();
         float* freed = sA + ((j + 2) % 3) * SA;   // A stage of k-tile j - 1
         if (t > 0) {
@@ -1276,7 +1283,7 @@ __global__ __launch_bounds__(512) void gemm_bf16_ring_kernel(GemmArgs p) {
         issue_w();                     // W(j + 1), before the stores
         if (t > 0) {
             epilogue(t - 1, freed);
-            if (HAS_BIAS) wait_vmcnt(vm - b_mark);
+            if (HAS_BIAS) wait_after(vm - b_mark);
         }
         if constexpr (HAS_BIAS) {
             const float* bs = freed + 8 * STAGE_WORDS + wave * BIAS_WORDS;
@@ -1297,7 +1304,7 @@ __global__ __launch_bounds__(512) void gemm_bf16_ring_kernel(GemmArgs p) {
         run_ktile(j, true);
         ++j;
         for (int kt = 1; kt < nk; ++kt, ++j) {
-            wait_vmcnt(vm - w_mark);
+            wait_after(vm - w_mark);
             lds_barrier();
             run_ktile(j, false);
         }

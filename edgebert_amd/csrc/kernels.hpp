@@ -322,6 +322,22 @@ __device__ __forceinline__ void wait_vmcnt(int n) {
     }
 }
 
+// wait_vmcnt for a count known to be one of a few values: a descending
+// ladder over those values (V0 > V1 > ...) waits until at most the largest
+// of them that is <= n is outstanding, else for everything.  That is the
+// exact wait when n is one of them and a longer one otherwise, and costs a
+// compare per value instead of wait_vmcnt's search over the counter's range.
+template <int V, int... Vs>
+__device__ __forceinline__ void wait_vmcnt_of(int n) {
+    static_assert(V >= 0 && V < 64, "vmcnt range");
+    if (n >= V) {
+        asm volatile("s_waitcnt vmcnt(%0)" ::"n"(V) : "memory");
+    } else {
+        if constexpr (sizeof...(Vs) > 0) wait_vmcnt_of<Vs...>(n);
+        else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    }
+}
+
 // This wave's LDS reads have returned; then the workgroup barrier.
 __device__ __forceinline__ void lds_barrier() {
     asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
