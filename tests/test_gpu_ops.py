@@ -253,6 +253,47 @@ def test_gemm_bf16_activations(env, M, N, K, epi, c16):
         np.testing.assert_allclose(got, want, rtol=0, atol=2e-5 * np.sqrt(K))
 
 
+@pytest.mark.parametrize("M,N,K,epi,pad", [
+    (20000, 3072, 768, 1, 0),    # 79 x 12 tiles: several per workgroup, ragged last row block, GELU
+    (70001, 256, 64, 0, 8),      # one k-tile per tile, 274 tiles, odd M, C rows 8 elements apart beyond N
+    (9000, 2304, 768, 3, 0),     # no bias
+    (33000, 768, 3072, 0, 0),    # long K: 48 k-tiles per tile
+])
+def test_gemm_bf16_ring_many_tiles(env, M, N, K, epi, pad):
+    """bf16 products with bf16 outputs over more tiles than workgroups: each
+    workgroup walks several tiles, so every tile boundary (the previous
+    tile's epilogue and buffer stores, the next tile's bias in its
+    accumulators, the three-stage A ring) is exercised.  Against torch's fp32
+    product of the same bf16 values (TF32 off), within one bf16 rounding;
+    the row padding past N must stay untouched."""
+    torch, eb, Nn, L = env
+    g = torch.Generator(device="cuda").manual_seed(M + N + K)
+    A = torch.randn(M, K, device="cuda", generator=g).to(torch.bfloat16)
+    W = (0.05 * torch.randn(N, K, device="cuda", generator=g)).to(torch.bfloat16)
+    bias = torch.randn(N, device="cuda", generator=g)
+    ldc = N + pad
+    C = torch.full((M, ldc), float("nan"), device="cuda", dtype=torch.bfloat16)
+    Nn.check(L.ebh_op_gemm_bf16(vp(A), K, vp(W), K, vp(bias) if epi != 3 else None, vp(C), ldc,
+                                Nn.EBH_DTYPE_BF16, M, N, K, epi, stream(torch)))
+    torch.cuda.synchronize()
+    prev = torch.backends.cuda.matmul.allow_tf32
+    torch.backends.cuda.matmul.allow_tf32 = False
+    try:
+        want = A.float() @ W.float().t()
+    finally:
+        torch.backends.cuda.matmul.allow_tf32 = prev
+    if epi != 3:
+        want = want + bias
+    if epi == 1:
+        want = torch.nn.functional.gelu(want, approximate="tanh")
+    got = C[:, :N].float()
+    err = (got - want).abs()
+    tol = 2 ** -8 * want.abs() + 1e-4 * K ** 0.5
+    assert bool((err <= tol).all()), f"max err {float(err.max()):.3e}"
+    if pad:
+        assert bool(torch.isnan(C[:, N:].float()).all())
+
+
 def test_f32_to_bf16_round_to_nearest_even(env):
     torch, eb, Nn, L = env
     rng = np.random.default_rng(3)
