@@ -74,18 +74,22 @@ def kernel_work(cfg, lengths, B: int, which: str, fused: bool = False, dtype: st
     4*T*H*2 bytes.  Row kernels: the HBM bytes the op must move at minimum
     (each operand read once, each result written once), in the activation
     encoding of the model (bf16 models keep the GEMM outputs and the residual
-    stream in bf16).  fused: the few-token layer's launches (few_fused).
+    stream in bf16).  Embeddings: a word row per token, but each of the
+    max(l) position rows once (every sequence shares them, so after the first
+    read they come from cache).  fused: the few-token layer's launches
+    (few_fused).
     """
     H, I = cfg.hidden_size, cfg.intermediate_size
     lengths = np.asarray(lengths, np.float64)
     T = float(lengths.sum())
+    P = float(lengths.max()) if lengths.size else 0.0   # distinct position rows
     if dtype == "bf16":
         if which == "attention":
             return 4.0 * T * H * 2, "hbm", "byte"
         if which == "layernorm":      # bf16 product and residual read, bf16 residual written
             return 3.0 * T * H * 2 + 3 * H * 4, "hbm", "byte"
-        if which == "embed":          # fp32 word / position rows in, bf16 row written
-            return T * (8 + 2 * H * 4 + H * 2) + 3 * H * 4, "hbm", "byte"
+        if which == "embed":          # fp32 word row in, bf16 row written per token
+            return T * (8 + H * 4 + H * 2) + P * H * 4 + 3 * H * 4, "hbm", "byte"
         if which == "pool":           # the bf16 residual stream once, one fp32 vector per sequence
             return T * H * 2 + B * H * 4 + (B + 1) * 4, "hbm", "byte"
     if fused and which == "attention":
@@ -104,8 +108,8 @@ def kernel_work(cfg, lengths, B: int, which: str, fused: bool = False, dtype: st
         return 4.0 * H * float((lengths ** 2).sum()), "mfma", "flop"
     if which == "layernorm":          # read the GEMM output row, write the normalised row
         return 2.0 * T * H * 4 + 2 * H * 4, "hbm", "byte"
-    if which == "embed":              # token id + position, word/position rows, written row
-        return T * (8 + 3 * H * 4) + 3 * H * 4, "hbm", "byte"
+    if which == "embed":              # token id + position, word row in, row written per token
+        return T * (8 + 2 * H * 4) + P * H * 4 + 3 * H * 4, "hbm", "byte"
     if which == "pool":               # every token row once, one vector per sequence
         return T * H * 4 + B * H * 4 + (B + 1) * 4, "hbm", "byte"
     raise KeyError(which)
