@@ -1220,18 +1220,37 @@ __global__ __launch_bounds__(512) void gemm_bf16_ring_kernel(GemmArgs p) {
     // Epilogue of local tile t (GELU or nothing: the bias is in the
     // accumulators), one 16-row block at a time through the wave's 2 KB of
     // the freed A stage `st`, then 16-byte buffer stores of whole row chunks.
+    // Every address is a lane constant of the epilogue plus a compile-time
+    // step: a store's descriptor starts at its 8-row group and ends at row M,
+    // so the lane offset (row within the group, column) is the same for all
+    // of the tile's stores, and rows past M fall outside the descriptor.
+    static_assert(CPW == 8 && ST_PASS * 64 == EROWS * CPW, "a store pass is 8 rows of 8 chunks");
     auto epilogue = [&](int t, float* st) __attribute__((always_inline)) {
         const int u = wg + t * G;
-        const int m0 = (u / ntiles_n) * BM, n0 = (u % ntiles_n) * BN;
-        const int valid = min(M - m0, BM);
-        const __amdgpu_buffer_rsrc_t cr = __builtin_amdgcn_make_buffer_rsrc(
-            reinterpret_cast<uint16_t*>(p.C) + (int64_t)m0 * p.ldc, (short)0,
-            (int)(uint32_t)((uint64_t)valid * p.ldc * 2), BUFFER_RSRC_WORD3);
-        // Lane-derived values opaque here: computed at the stores, not held
+        const int ws = __builtin_amdgcn_readfirstlane(wave);
+        const int wrow = (u / ntiles_n) * BM + (ws / WAVES_N) * WM;   // the wave tile's first C row
+        const int n0 = (u % ntiles_n) * BN;
+        // Lane-derived values opaque here: formed at the epilogue, not held
         // across the k-loop (the last tile's epilogue follows it).
-        int el = lane, er = r16, eq = q16, ew = wave;
-        asm volatile("" : "+v"(el), "+v"(er), "+v"(eq), "+v"(ew));
-        char* cw = reinterpret_cast<char*>(st + ew * STAGE_WORDS);
+        int el = lane;
+        asm volatile("" : "+v"(el));
+        const int er = el & 15, eq = el >> 4;   // C fragment: row er, columns 4 eq .. 4 eq + 3 of a block
+        const int sr = el >> 3, sc = el & 7;    // store: row sr of an 8-row group, 16-byte chunk sc
+        char* const cw = reinterpret_cast<char*>(st + ws * STAGE_WORDS);
+        // Fragment writes: row er, chunk (2 j + eq / 2) ^ (er & 7), half eq & 1;
+        // 2 j + b = 2 j ^ b for b < 2, so the chunk's byte offset is wx ^ 32 j.
+        char* const wr = cw + er * (2 * WN) + 8 * (eq & 1);
+        const int wx = ((eq >> 1) ^ (er & 7)) << 4;
+        // Row reads: row 8 ps + sr, chunk sc ^ sr.
+        const char* const rd = cw + sr * (2 * WN) + ((sc ^ sr) << 4);
+        const int col = n0 + (ws % WAVES_N) * WN + 8 * sc;
+        const uint32_t voff = col < N ? (uint32_t)((sr * p.ldc + col) * 2) : 0xFFFFFFF0u;
+        // Rows of the wave tile that exist (at most WM; <= 0 past M), and the
+        // bytes of a C row: wave-uniform, so the descriptors stay scalar (a
+        // descriptor in VGPRs makes the compiler loop over the lanes).
+        const int wv = __builtin_amdgcn_readfirstlane(M - wrow);
+        const int rowb = p.ldc * 2;
+        uint16_t* const cbase = reinterpret_cast<uint16_t*>(p.C);
 #pragma unroll
         for (int i = 0; i < FM16; ++i) {
 #pragma unroll
@@ -1243,17 +1262,18 @@ __global__ __launch_bounds__(512) void gemm_bf16_ring_kernel(GemmArgs p) {
                     v.z = gelu_tanh_fast(v.z); v.w = gelu_tanh_fast(v.w);
                 }
                 const uint2 h = make_uint2(pack_bf16x2(v.x, v.y), pack_bf16x2(v.z, v.w));
-                *reinterpret_cast<uint2*>(cw + er * (2 * WN) + (((2 * j + (eq >> 1)) ^ (er & 7)) << 4) +
-                                          8 * (eq & 1)) = h;
+                *reinterpret_cast<uint2*>(wr + (wx ^ (32 * j))) = h;
             }
 #pragma unroll
             for (int ps = 0; ps < ST_PASS; ++ps) {
-                const int q = ps * 64 + el, r = q / CPW, c = q - r * CPW;
-                const uint4 d = *reinterpret_cast<const uint4*>(cw + r * (2 * WN) + ((c ^ (r & 7)) << 4));
-                const int row = (ew / WAVES_N) * WM + i * EROWS + r, col = n0 + (ew % WAVES_N) * WN + 8 * c;
-                const uint32_t off = row < valid && col < N ? (uint32_t)((row * p.ldc + col) * 2) : 0xFFFFFFF0u;
+                const uint4 d = *reinterpret_cast<const uint4*>(rd + ps * 8 * (2 * WN));
+                const int r0 = i * EROWS + ps * 8;                    // the group's first row in the wave tile
+                const int left = wv - r0;
+                const int bytes = left >= 8 ? 8 * rowb : (left > 0 ? left * rowb : 0);
+                const __amdgpu_buffer_rsrc_t cr = __builtin_amdgcn_make_buffer_rsrc(
+                    cbase + (int64_t)(wrow + r0) * p.ldc, (short)0, bytes, BUFFER_RSRC_WORD3);
                 typedef unsigned int u4v __attribute__((ext_vector_type(4)));
-                __builtin_amdgcn_raw_buffer_store_b128(u4v{d.x, d.y, d.z, d.w}, cr, off, 0, 2 /* nt */);
+                __builtin_amdgcn_raw_buffer_store_b128(u4v{d.x, d.y, d.z, d.w}, cr, voff, 0, 2 /* nt */);
             }
         }
         vm += N_ST;
