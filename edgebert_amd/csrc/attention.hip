@@ -195,7 +195,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(HD == 32 ? 
         }
         __syncthreads();
         if (PREFETCH && c + 1 < nchunks) load_chunk((c + 1) * KC);
-        attend_chunk<HD>(Ks, Vs, qf, c_exp, l32, half, min(len - c * KC, KC), o, m_run, l_run, c == 0);
+        // A wave whose 32 queries all lie past the sequence end (the last
+        // query block of a ragged sequence) only helps load K and V.
+        if (q0 < len)
+            attend_chunk<HD>(Ks, Vs, qf, c_exp, l32, half, min(len - c * KC, KC), o, m_run, l_run, c == 0);
     }
 
     // Normalise by the row sum (both lane halves hold partial sums) and store:
@@ -320,6 +323,9 @@ __global__ __launch_bounds__(256) void attention_bf16_kernel(const uint16_t* __r
             }
         }
         __syncthreads();
+        // A wave whose 32 queries all lie past the sequence end only helps
+        // load K and V.
+        if (q0 >= len) continue;
 
         const int nkb = min(4, (len - kbase + 31) / 32);  // 32-key blocks holding real keys
         v16f sc[4];
@@ -500,6 +506,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
     }
     wait_vmcnt(NLD);   // this wave's Q and K loads (its V loads may be in flight)
     __syncthreads();
+    // A wave whose 32 queries all lie past the sequence end skips the scores
+    // and P.V; it still meets the barrier below.
+    const bool active = wave * 32 < len;
     // This lane's query as the B operand: dims 16s + 8*half .. +7.
     const int qr = wave * 32 + l32;
     v8s_t qf[NS];
@@ -507,7 +516,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
     for (int s = 0; s < NS; ++s)
         qf[s] = *reinterpret_cast<const v8s_t*>(Qs + qr * HD + 8 * ((2 * s + half) ^ chunk_swizzle16<CPR>(qr)));
 
-    const int nkb = (len + 31) / 32;     // 32-key blocks holding real keys
+    const int nkb = active ? (len + 31) / 32 : 0;   // 32-key blocks holding real keys
     // S^T = K . Q^T: the four 32-key blocks' MFMA chains side by side.
     v16f sc[4];
 #pragma unroll
