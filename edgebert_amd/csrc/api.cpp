@@ -153,8 +153,11 @@ struct ebh_model {
     uint64_t graph_clock = 0;
     bool graph_replay = true;
     // ebh_encode_device_noalloc has run on this model: ebh_synchronize also
-    // reads the id-range flag of the device's static scratch workspace
+    // reads noalloc_err, the id-range flag those forwards raise (a word of
+    // the weight block, so each model has its own and the call allocates
+    // nothing)
     bool noalloc_used = false;
+    int* noalloc_err = nullptr;
     // profiling of one kernel family
     int prof_kind = EBH_PROF_NONE;
     std::vector<ProfPair> prof_events;
@@ -689,7 +692,8 @@ int check_dims(const ebh_model* m, int B, int S) {
 
 // ---------------------------------------------------------------------------
 // Static scratch workspace of ebh_encode_device_noalloc: the activations of
-// one forward (laid out by layout_workspace, id-range flag first), held by
+// one forward (laid out by layout_workspace; the id-range flag is the
+// model's own, in its weight block), held by
 // every device the library runs on until the process ends.  Host code never
 // uses the array's name as an address (on the host it is only a stand-in):
 // ebh_finalize looks its device address up once per device with
@@ -703,18 +707,16 @@ std::mutex g_scratch_mu;
 char* g_scratch_ptr[MAX_DEVICES] = {};   // device address of `scratch` per device
 
 // Called by ebh_finalize with the model's device current: look the array up
-// on this device once and clear its id-range flag (the word every no-
-// allocation forward's flag occupies), ordered before any later work of the
-// model by the stream synchronisation that follows.
-int setup_scratch(int dev, hipStream_t s) {
+// on this device once.  (Its first word, the id-range flag slot of the
+// workspace layout, is unused: each model's no-allocation forwards raise
+// that model's own flag.)
+int setup_scratch(int dev) {
     if (dev < 0 || dev >= MAX_DEVICES) return fail(EBH_ERR_STATE, "device %d beyond %d devices", dev, MAX_DEVICES);
     std::lock_guard<std::mutex> lk(g_scratch_mu);
     if (g_scratch_ptr[dev]) return EBH_OK;
     void* p = nullptr;
     HIP_TRY(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
     if (!p) return fail(EBH_ERR_HIP, "hipGetSymbolAddress returned no address for the scratch workspace");
-    HIP_TRY(ebh::launch_zero_words(p, 1, s));
-    HIP_TRY(hipStreamSynchronize(s));
     g_scratch_ptr[dev] = static_cast<char*>(p);
     return EBH_OK;
 }
@@ -816,6 +818,7 @@ static void release_partial_finalize(ebh_model* m) {
     if (m->done) (void)hipEventDestroy(m->done);
     if (m->stream) (void)hipStreamDestroy(m->stream);
     m->wbase = nullptr;
+    m->noalloc_err = nullptr;
     m->done = nullptr;
     m->stream = nullptr;
     m->device = -1;
@@ -871,11 +874,12 @@ static int finalize_locked(ebh_model* m, int32_t dtype) {
         o.ln2_g = take(H * 4); o.ln2_b = take(H * 4);
     }
     const size_t oClsW = has_cw ? take(H * 4) : 0, oClsB = has_cw ? take(4) : 0;
+    const size_t oNoallocErr = take(4);            // id-range flag of ebh_encode_device_noalloc
 
     HIP_TRY(hipGetDevice(&m->device));
     HIP_TRY(hipStreamCreateWithFlags(&m->stream, hipStreamNonBlocking));
     HIP_TRY(hipEventCreateWithFlags(&m->done, hipEventDisableTiming));
-    if ((rc0 = setup_scratch(m->device, m->stream))) return rc0;
+    if ((rc0 = setup_scratch(m->device))) return rc0;
     HIP_TRY(hipMalloc(&m->wbase, off));
     char* b = static_cast<char*>(m->wbase);
 
@@ -948,6 +952,7 @@ static int finalize_locked(ebh_model* m, int32_t dtype) {
         EBH_UP(oClsB, "classifier.bias", false);
     }
 #undef EBH_UP
+    HIP_TRY(ebh::launch_zero_words(b + oNoallocErr, 1, st));
     HIP_TRY(hipStreamSynchronize(st));
 
     m->word = (float*)(b + oWord);
@@ -958,6 +963,7 @@ static int finalize_locked(ebh_model* m, int32_t dtype) {
     m->cross_encoder = has_cw;
     m->cls_w = has_cw ? (float*)(b + oClsW) : nullptr;
     m->cls_b = has_cw ? (float*)(b + oClsB) : nullptr;
+    m->noalloc_err = (int*)(b + oNoallocErr);
     m->layers.resize(L);
     for (size_t l = 0; l < L; ++l) {
         const Off& o = lo[l];
@@ -1116,6 +1122,7 @@ int ebh_encode_device_noalloc(ebh_model* m, const int32_t* ids, const int32_t* m
         HIP_TRY(ebh::launch_zero_words(out, (int64_t)B * m->cfg.hidden_size, s));
     } else {
         layout_workspace(m, T, B, base, w);
+        w.err = m->noalloc_err;   // this model's flag, not the shared array's
         if ((rc = enqueue_kernels(m, w, ids, mask, B, S, normalize ? 1 : 0, out, s, nullptr, -1, false)))
             return rc;
     }
@@ -1214,8 +1221,7 @@ int ebh_synchronize(ebh_model* m) {
     HIP_TRY(hipSetDevice(m->device));
     if (m->has_done) HIP_TRY(hipEventSynchronize(m->done));
     int err = 0;
-    for (int* flag : {m->ws.base ? m->ws.err : nullptr,
-                      m->noalloc_used ? reinterpret_cast<int*>(scratch_ptr(m->device)) : nullptr}) {
+    for (int* flag : {m->ws.base ? m->ws.err : nullptr, m->noalloc_used ? m->noalloc_err : nullptr}) {
         if (!flag) continue;
         int e = 0;
         HIP_TRY(hipMemcpy(&e, flag, 4, hipMemcpyDeviceToHost));

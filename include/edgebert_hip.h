@@ -153,9 +153,10 @@ EBH_API int ebh_encode_device(ebh_model* m, const int32_t* ids, const int32_t* m
  * 9k in bf16, e.g. 56 x 128; BERT-base about 3.5k in fp32, 4.4k in bf16).
  * Every call on one device shares that array: calls that overlap on a device
  * (other models, other streams, other threads) race; calls on one model are
- * ordered as ebh_encode_device's are.  Its id-range flag is the first word of
- * the array, reported and cleared by ebh_synchronize of a model that ran this
- * entry point.  ebh_last_tokens does not cover these forwards. */
+ * ordered as ebh_encode_device's are.  A bad id raises the calling model's
+ * own id-range flag (a word ebh_finalize reserves in the model's weight
+ * block), which that model's ebh_synchronize reports and clears; other
+ * models never see it.  ebh_last_tokens does not cover these forwards. */
 #define EBH_NOALLOC_SCRATCH_BYTES (128u << 20)
 EBH_API int ebh_encode_device_noalloc(ebh_model* m, const int32_t* ids, const int32_t* mask, int32_t B,
                                       int32_t S, int32_t normalize, float* out, void* stream);

@@ -3,7 +3,8 @@ against the allocating ebh_encode_device on the same inputs: two calls in a
 row, the second smaller, bit-identical results (the same kernels with the same
 arguments, only the workspace differs); sizes beyond the static scratch are
 rejected; no device memory is taken; the id-range flag is reported by
-ebh_synchronize.  Passes alone in a fresh process and after the other tests."""
+ebh_synchronize of the model that raised it, and of no other.  Passes alone in
+a fresh process and after the other tests."""
 import ctypes
 
 import numpy as np
@@ -108,3 +109,38 @@ def test_noalloc_reports_bad_ids_on_synchronize(env):
         assert torch.isfinite(out).all()
     finally:
         m.close()
+
+
+def test_noalloc_bad_id_is_reported_by_its_own_model_only(env):
+    """Two models: a bad id in model a's no-allocation forward is reported by
+    a's ebh_synchronize, not by b's (b's own forwards are clean), and b's
+    results are those of a clean run.  The two forwards share the device's
+    scratch array, so they must not overlap: each model runs on its own
+    stream here, and the device is synchronised between them."""
+    torch, eb, N, synth, w = env
+    cfg = synth.MINILM_L6
+    s = torch.cuda.current_stream().cuda_stream
+    a = eb.Model.from_weights(w, cfg, "fp32")
+    b = eb.Model.from_weights(w, cfg, "fp32")
+    try:
+        ids = torch.full((2, 24), 101, dtype=torch.int32, device="cuda")
+        mask = torch.ones_like(ids)
+        bad = ids.clone()
+        bad[1, 3] = cfg.vocab_size + 11
+        out_a = torch.empty((2, cfg.hidden_size), device="cuda")
+        out_b = torch.empty((2, cfg.hidden_size), device="cuda")
+        want = torch.empty((2, cfg.hidden_size), device="cuda")
+        b.set_graph_replay(False)
+        b.encode_device(ids.data_ptr(), mask.data_ptr(), 2, 24, want.data_ptr(), True, s)
+        b.synchronize()
+        N.check(_noalloc(N, a, bad, mask, 2, 24, out_a, s))
+        torch.cuda.synchronize()                             # a's forward done, its flag raised
+        N.check(_noalloc(N, b, ids, mask, 2, 24, out_b, s))
+        b.synchronize()                                      # clean: a's flag is not b's
+        assert torch.equal(out_b, want)
+        with pytest.raises(eb.EbhError, match="out of range"):
+            a.synchronize()
+        a.synchronize()                                      # reported once, then cleared
+    finally:
+        a.close()
+        b.close()
