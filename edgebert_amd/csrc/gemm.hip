@@ -591,38 +591,62 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_persistent_kernel
     };
 
     // Epilogue of local tile t: bias (+ GELU), C through LDS stage `cs`, float4 stores.
-    // Bias (+ GELU) of one float4 and its store at (row, gcol).
-    auto put4 = [&](float* Cs, float4 v, const float4& b4, int row, int gcol) __attribute__((always_inline)) {
-        if (HAS_BIAS) { v.x += b4.x; v.y += b4.y; v.z += b4.z; v.w += b4.w; }
-        if constexpr (EPI == EPI_BIAS_GELU) {
-            v.x = gelu_tanh_fast(v.x); v.y = gelu_tanh_fast(v.y);
-            v.z = gelu_tanh_fast(v.z); v.w = gelu_tanh_fast(v.w);
-        }
-        if (gcol < N && row < M) {   // N % 4 == 0: all 4 columns or none
-            if constexpr (OUT16) {
-                uint2 h;
-                h.x = (uint32_t)f32_to_bf16_rne(v.x) | ((uint32_t)f32_to_bf16_rne(v.y) << 16);
-                h.y = (uint32_t)f32_to_bf16_rne(v.z) | ((uint32_t)f32_to_bf16_rne(v.w) << 16);
-                *reinterpret_cast<uint2*>(reinterpret_cast<uint16_t*>(Cs) + (int64_t)row * p.ldc + gcol) = h;
-            } else {
-                *reinterpret_cast<float4*>(Cs + (int64_t)row * p.ldc + gcol) = v;
-            }
+    // One row group's store: the descriptor starts at C row g0 (wave-uniform)
+    // and holds min(M - g0, span) rows, so a lane whose row in the group lies
+    // past M (or whose offset is the out-of-range value) is not written.
+    // The lane offsets are constants of the epilogue: no per-store row
+    // arithmetic, which on this chip adds to the fp32 MFMA time.
+    constexpr int CES = OUT16 ? 2 : 4;  // bytes per C element
+    // wrow, wv: the wave tile's first C row and the rows of it that exist
+    // (wave-uniform: a descriptor in VGPRs makes the compiler loop over lanes).
+    auto store_group = [&](char* cb, int wrow, int wv, int r0, int span, uint32_t voff, float4 v)
+                           __attribute__((always_inline)) {
+        const int rowb = p.ldc * CES, left = wv - r0, g0 = wrow + r0;
+        const int bytes = left >= span ? span * rowb : (left > 0 ? left * rowb : 0);
+        const __amdgpu_buffer_rsrc_t cr =
+            __builtin_amdgcn_make_buffer_rsrc(cb + (int64_t)g0 * rowb, (short)0, bytes, BUFFER_RSRC_WORD3);
+        typedef unsigned int u4v __attribute__((ext_vector_type(4)));
+        typedef unsigned int u2v __attribute__((ext_vector_type(2)));
+        if constexpr (OUT16) {
+            const u2v h = {(uint32_t)f32_to_bf16_rne(v.x) | ((uint32_t)f32_to_bf16_rne(v.y) << 16),
+                           (uint32_t)f32_to_bf16_rne(v.z) | ((uint32_t)f32_to_bf16_rne(v.w) << 16)};
+            __builtin_amdgcn_raw_buffer_store_b64(h, cr, voff, 0, 0);
+        } else {
+            __builtin_amdgcn_raw_buffer_store_b128(
+                u4v{__float_as_uint(v.x), __float_as_uint(v.y), __float_as_uint(v.z), __float_as_uint(v.w)}, cr,
+                voff, 0, 0);
         }
     };
     // FLAT epilogue: per 16-row half of each 32-row block (MFMA rows r = 8h ..
     // 8h+7 hold rows 16h .. 16h+15), C through the wave's 16 x WN slot of LDS
     // stage `cs`, then float4 q = pass * 64 + lane of those rows in row-major
-    // order.
+    // order.  The lane's (row, column) repeats every PP passes (64 PP float4
+    // are whole rows), so each of the PP patterns has its own lane constants.
     auto epilogue_flat = [&](int t, const float* cs_base) __attribute__((always_inline)) {
         const int u = wg + t * G, split = u / ntiles, tile = u - split * ntiles;
-        float* const Cs = p.C + (int64_t)split * p.split_stride;
+        char* const cb = reinterpret_cast<char*>(p.C + (int64_t)split * p.split_stride);
         const int m0 = (tile / ntiles_n) * BM, n0 = (tile - (tile / ntiles_n) * ntiles_n) * BN;
         const float* bslot = smem + NSTAGE * STAGE + ((t & 1) * NW + wave) * BIAS_SLOT;
         float* cw = const_cast<float*>(cs_base) + wave * (16 * WN);
         constexpr int NPASS = 4 * WN / 64;
-        // lane-derived offsets opaque here (computed at the stores, not held)
+        constexpr int PP = C4 / (C4 % 64 == 0 ? 64 : (C4 % 32 == 0 ? 32 : (C4 % 16 == 0 ? 16 : 8)));
+        constexpr int RPG = 64 * PP / C4;              // rows per PP passes
+        constexpr int SPAN = 64 / C4 + 2;              // rows one store can touch, at most
+        static_assert(C4 % 8 == 0 && NPASS % PP == 0 && (64 * PP) % C4 == 0, "FLAT pass pattern");
+        // lane-derived offsets opaque here (formed at the epilogue, not held)
         int fl = lane, fl32 = l32, fhalf = half;
         asm volatile("" : "+v"(fl), "+v"(fl32), "+v"(fhalf));
+        const int wrow = __builtin_amdgcn_readfirstlane(m0 + wm * WM), wv = __builtin_amdgcn_readfirstlane(M - wrow);
+        int ldo[PP], bo[PP];
+        uint32_t vo[PP];
+#pragma unroll
+        for (int pp = 0; pp < PP; ++pp) {
+            const int q = 64 * pp + fl, lr = q / C4, c = 4 * (q - lr * C4);
+            const int gc = n0 + wn * WN + c;
+            ldo[pp] = lr * WN + c;
+            bo[pp] = c;
+            vo[pp] = gc < N ? (uint32_t)(((lr - (64 * pp) / C4) * p.ldc + gc) * CES) : 0xFFFFFFF0u;
+        }
 #pragma unroll
         for (int i = 0; i < FM; ++i)
 #pragma unroll
@@ -634,29 +658,35 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_persistent_kernel
                         cw[(8 * (rr >> 2) + 4 * fhalf + (rr & 3)) * WN + j * 32 + fl32] = acc[i][j][8 * h + rr];
 #pragma unroll
                 for (int ps = 0; ps < NPASS; ++ps) {
-                    const int q = ps * 64 + fl, lr = q / C4, c = 4 * (q - lr * C4);
-                    const float4 v = *reinterpret_cast<const float4*>(cw + lr * WN + c);
-                    float4 b4 = make_float4(0, 0, 0, 0);
-                    if (HAS_BIAS) b4 = *reinterpret_cast<const float4*>(bslot + c);
-                    put4(Cs, v, b4, m0 + wm * WM + i * 32 + 16 * h + lr, n0 + wn * WN + c);
+                    const int pp = ps % PP, k = ps / PP;
+                    float4 v = *reinterpret_cast<const float4*>(cw + ldo[pp] + k * RPG * WN);
+                    if (HAS_BIAS) {
+                        const float4 b4 = *reinterpret_cast<const float4*>(bslot + bo[pp]);
+                        v.x += b4.x; v.y += b4.y; v.z += b4.z; v.w += b4.w;
+                    }
+                    if constexpr (EPI == EPI_BIAS_GELU) {
+                        v.x = gelu_tanh_fast(v.x); v.y = gelu_tanh_fast(v.y);
+                        v.z = gelu_tanh_fast(v.z); v.w = gelu_tanh_fast(v.w);
+                    }
+                    store_group(cb, wrow, wv, i * 32 + 16 * h + (64 * pp) / C4 + k * RPG, SPAN, vo[pp], v);
                 }
             }
     };
     auto epilogue_tile = [&](int t, const float* cs_base) {
         const int u = wg + t * G, split = u / ntiles, tile = u - split * ntiles;
-        float* const Cs = p.C + (int64_t)split * p.split_stride;
+        char* const cb = reinterpret_cast<char*>(p.C + (int64_t)split * p.split_stride);
         const int m0 = (tile / ntiles_n) * BM, n0 = (tile - (tile / ntiles_n) * ntiles_n) * BN;
-        // The lane's place in the tile, opaque here: the row addresses derived
-        // from it are computed at the stores, not held across the k-loop.
+        // The lane's place in the tile, opaque here: the offsets derived from
+        // it are formed at the epilogue, not held across the k-loop.
         int er = e_r, ec = e_c;
         asm volatile("" : "+v"(er), "+v"(ec));
         const int gc = n0 + wn * WN + ec;
-        const bool col_ok = gc < N;  // N % 4 == 0: all 4 columns or none
         float4 bias4 = make_float4(0, 0, 0, 0);
         if (HAS_BIAS)
             bias4 = *reinterpret_cast<const float4*>(smem + NSTAGE * STAGE + ((t & 1) * NW + wave) * BIAS_SLOT + ec);
         float* cw = const_cast<float*>(cs_base) + wave * (32 * WN);
-        const int grow0 = m0 + wm * WM + er;
+        const int wrow = __builtin_amdgcn_readfirstlane(m0 + wm * WM), wv = __builtin_amdgcn_readfirstlane(M - wrow);
+        const uint32_t voff = gc < N ? (uint32_t)((er * p.ldc + gc) * CES) : 0xFFFFFFF0u;   // N % 4 == 0
 #pragma unroll
         for (int i = 0; i < FM; ++i) {
 #pragma unroll
@@ -672,17 +702,7 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_persistent_kernel
                     v.x = gelu_tanh_fast(v.x); v.y = gelu_tanh_fast(v.y);
                     v.z = gelu_tanh_fast(v.z); v.w = gelu_tanh_fast(v.w);
                 }
-                const int row = grow0 + i * 32 + qq * RPP;
-                if (col_ok && row < M) {
-                    if constexpr (OUT16) {
-                        uint2 h;
-                        h.x = (uint32_t)f32_to_bf16_rne(v.x) | ((uint32_t)f32_to_bf16_rne(v.y) << 16);
-                        h.y = (uint32_t)f32_to_bf16_rne(v.z) | ((uint32_t)f32_to_bf16_rne(v.w) << 16);
-                        *reinterpret_cast<uint2*>(reinterpret_cast<uint16_t*>(Cs) + (int64_t)row * p.ldc + gc) = h;
-                    } else {
-                        *reinterpret_cast<float4*>(Cs + (int64_t)row * p.ldc + gc) = v;
-                    }
-                }
+                store_group(cb, wrow, wv, i * 32 + qq * RPP, RPP, voff, v);
             }
         }
     };
