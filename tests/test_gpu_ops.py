@@ -115,6 +115,8 @@ def test_gemm_f32_row_stride_past_32bit_offsets(env):
     (40000, 512, 160, 3),      # 256 x 256 tiles, no bias, 5 k-tiles
     (9000, 1024, 384, 1),      # 128 x 128 tiles beside the 128 x 384 case (N not whole panels)
     (500, 256, 96, 0),         # K % 64 != 0: 32-deep k-tiles
+    (4100, 1000, 384, 1),      # 128 x 128 tiles, N past the last whole panel, ragged rows (GELU)
+    (1000, 200, 256, 3),       # 64 x 64 tiles (few per CU), N past the last whole panel
 ])
 def test_gemm_f32_dispatch_paths(env, M, N, K, epi):
     """The tile configurations chosen for many tokens, each against the float64
