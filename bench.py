@@ -1,4 +1,5 @@
-"""Throughput of the gfx950 BERT encoder forward (BASELINE.json metric).
+"""Throughput of the gfx950 BERT encoder forward: sentences/s at MiniLM-L6 shape,
+batch 256 x seq 128, fp32, with the p50 batch latency.
 
 One step = one ``ebh_encode_device`` forward of the whole batch (embeddings ->
 L layers -> mean pool -> L2 normalise) over ids / mask already resident in
@@ -27,7 +28,7 @@ reference uses.
 
 ``kernels`` gives every kernel family of the headline forward the same way as
 ``roofline`` (HIP events, fraction of its roofline).  ``configs`` holds the
-other BASELINE configs (c5, c4, c2, c1 by default), each timed after the
+other benchmark configs (c5, c4, c2, c1 by default), each timed after the
 headline with its own model exactly as the headline is (``value``,
 ``ms_per_step``, p50), with its dominant kernel family as ``roofline`` and
 every family under ``kernels``; ``value`` and ``metric`` stay on c3.
@@ -410,7 +411,8 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU only; --gpus {args.gpus} is not supported "
-              "(the path shards as pure data parallelism over the batch, see DESIGN.md)",
+              "(the forward shards as pure data parallelism over the batch: one process per GPU, "
+              "each with its own slice of sentences)",
               file=sys.stderr)
         sys.exit(2)
 
