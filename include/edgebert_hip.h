@@ -4,8 +4,8 @@
  * Drop-in for the body of EdgeBERT's `Model::forward` plus the normalisation
  * tail of `encode_uncached` (/root/reference/src/lib.rs:588-666).  The host
  * tokenizer and the public `encode` / cache logic stay with the caller; a Rust
- * `hip` backend binds these symbols with `extern "C"` (the binding is shown in
- * INTEGRATION.md).
+ * `hip` backend binds these symbols with `extern "C"`, one declaration per
+ * function below with the same parameter types in the same order.
  *
  * Conventions
  *  - Every function returns EBH_OK (0) on success or a negative EBH_ERR_*

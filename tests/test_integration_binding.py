@@ -1,4 +1,5 @@
-"""The Rust binding printed in INTEGRATION.md against the C ABI it binds.
+"""The Rust binding printed in the repository's integration guide against the C
+ABI it binds.
 
 No Rust toolchain exists here, so the `hip` module cannot be compiled.  This
 test parses its `extern "C"` block and its `#[repr(C)]` config struct and
