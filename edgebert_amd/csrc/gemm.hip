@@ -334,11 +334,21 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_persistent_kernel
     const int S = p.splits > 1 ? p.splits : 1;
     const int nwork = ntiles * S;
     const int nk = p.K / BK / S;                  // k-tiles per work item
-    // Workgroup b runs on XCD b % 8: renumber so each XCD's workgroups take
-    // consecutive tiles (N-fastest), which share A row panels in that XCD's L2.
+    // Workgroup b runs on XCD b % 8.  Each XCD takes an eighth of the work
+    // items as one consecutive range (N-fastest tiles, which share A row
+    // panels in that XCD's L2), and its G / 8 workgroups walk the range in
+    // steps of G / 8.  When the items are not a multiple of G, every XCD's
+    // range ends in a partial step, so the last step's items spread over all
+    // XCDs instead of filling the first ones twice.
     const int G = gridDim.x;
-    const int wg = (G & 7) == 0 ? (blockIdx.x & 7) * (G >> 3) + (blockIdx.x >> 3) : blockIdx.x;
-    const int my_tiles = wg < nwork ? (nwork - wg + G - 1) / G : 0;
+    int u0 = blockIdx.x, ustep = G, uend = nwork;
+    if ((G & 7) == 0) {
+        const int x = blockIdx.x & 7;
+        ustep = G >> 3;
+        u0 = (int)((int64_t)x * nwork / 8) + (blockIdx.x >> 3);
+        uend = (int)((int64_t)(x + 1) * nwork / 8);
+    }
+    const int my_tiles = u0 < uend ? (uend - u0 + ustep - 1) / ustep : 0;
     const int total = my_tiles * nk;
     if (total == 0) return;  // uniform over the workgroup
 
@@ -375,7 +385,7 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_persistent_kernel
     const float* bias_src = nullptr;
     int nit = 0;
     auto point_at = [&](int it) {
-        const int u = wg + (it / nk) * G, split = u / ntiles, t = u - split * ntiles;
+        const int u = u0 + (it / nk) * ustep, split = u / ntiles, t = u - split * ntiles;
         const int kt = split * nk + it - (it / nk) * nk;
         const int mt = t / ntiles_n, m0 = mt * BM, n0 = (t - mt * ntiles_n) * BN;
 #pragma unroll
@@ -507,7 +517,7 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_persistent_kernel
     // (v - mean) * (1 / sqrt(var + eps)) * gamma + beta.  `ex` is a consumed
     // LDS stage (the exchange buffers).
     auto epilogue_ln = [&](int t, float* ex) __attribute__((always_inline)) {
-        const int m0 = (wg + t * G) * BM;
+        const int m0 = (u0 + t * ustep) * BM;
         const float* bsl = smem + NSTAGE * STAGE + ((t & 1) * NW + wave) * BIAS_SLOT + l32;
         const int col = wn * WN + l32;
         // R and C are [M, BN] (row stride BN), read and written through buffer
@@ -623,7 +633,7 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_persistent_kernel
     // order.  The lane's (row, column) repeats every PP passes (64 PP float4
     // are whole rows), so each of the PP patterns has its own lane constants.
     auto epilogue_flat = [&](int t, const float* cs_base) __attribute__((always_inline)) {
-        const int u = wg + t * G, split = u / ntiles, tile = u - split * ntiles;
+        const int u = u0 + t * ustep, split = u / ntiles, tile = u - split * ntiles;
         char* const cb = reinterpret_cast<char*>(p.C + (int64_t)split * p.split_stride);
         const int m0 = (tile / ntiles_n) * BM, n0 = (tile - (tile / ntiles_n) * ntiles_n) * BN;
         const float* bslot = smem + NSTAGE * STAGE + ((t & 1) * NW + wave) * BIAS_SLOT;
@@ -673,7 +683,7 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_persistent_kernel
             }
     };
     auto epilogue_tile = [&](int t, const float* cs_base) {
-        const int u = wg + t * G, split = u / ntiles, tile = u - split * ntiles;
+        const int u = u0 + t * ustep, split = u / ntiles, tile = u - split * ntiles;
         char* const cb = reinterpret_cast<char*>(p.C + (int64_t)split * p.split_stride);
         const int m0 = (tile / ntiles_n) * BM, n0 = (tile - (tile / ntiles_n) * ntiles_n) * BN;
         // The lane's place in the tile, opaque here: the offsets derived from
@@ -715,7 +725,7 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_persistent_kernel
     // neither the 8-byte writes down a column nor the 16-byte reads along the
     // rows collide on a bank) and leave as 16-byte row-contiguous stores.
     auto epilogue_packed = [&](int t, const float* cs_base) __attribute__((always_inline)) {
-        const int u = wg + t * G, split = u / ntiles, tile = u - split * ntiles;
+        const int u = u0 + t * ustep, split = u / ntiles, tile = u - split * ntiles;
         uint16_t* const Cs = reinterpret_cast<uint16_t*>(p.C) + (int64_t)split * p.split_stride;
         const int m0 = (tile / ntiles_n) * BM, n0 = (tile - (tile / ntiles_n) * ntiles_n) * BN;
         const float* bslot = smem + NSTAGE * STAGE + ((t & 1) * NW + wave) * BIAS_SLOT;
@@ -768,7 +778,7 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_persistent_kernel
     // wave-tile row 16 i + r16, column 16 j + 4 q16 + e.  Two row blocks (32
     // rows) at a time go through the wave's LDS slot as in epilogue_packed.
     auto epilogue_packed16 = [&](int t, const float* cs_base) __attribute__((always_inline)) {
-        const int u = wg + t * G, split = u / ntiles, tile = u - split * ntiles;
+        const int u = u0 + t * ustep, split = u / ntiles, tile = u - split * ntiles;
         uint16_t* const Cs = reinterpret_cast<uint16_t*>(p.C) + (int64_t)split * p.split_stride;
         const int m0 = (tile / ntiles_n) * BM, n0 = (tile - (tile / ntiles_n) * ntiles_n) * BN;
         const float* bslot = smem + NSTAGE * STAGE + ((t & 1) * NW + wave) * BIAS_SLOT;
@@ -818,7 +828,7 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_persistent_kernel
     // fp32 output of the 16x16x32 blocks (the op-level bf16 GEMM with an fp32
     // C): each lane's four consecutive columns of a row as one float4 store.
     auto epilogue_direct16 = [&](int t) __attribute__((always_inline)) {
-        const int u = wg + t * G, split = u / ntiles, tile = u - split * ntiles;
+        const int u = u0 + t * ustep, split = u / ntiles, tile = u - split * ntiles;
         float* const Cs = p.C + (int64_t)split * p.split_stride;
         const int m0 = (tile / ntiles_n) * BM, n0 = (tile - (tile / ntiles_n) * ntiles_n) * BN;
         const float* bslot = smem + NSTAGE * STAGE + ((t & 1) * NW + wave) * BIAS_SLOT;
@@ -1713,6 +1723,16 @@ hipError_t launch_gemm_f32(const GemmArgs& a, int epi, hipStream_t s) {
     //    k-tiles, 8 waves of 64 x 96.  Both wide tiles load far fewer bytes per
     //    flop than 128 x 128 (QKV 297 -> 262 us at 128 x 384, 252 -> 243 us
     //    at 256 x 192; FFN up 338 -> 319 us at 128 x 384);
+    //  * but where either wide tile would make fewer than two rounds of
+    //    workgroups by the padded row count, and N is whole 96-column panels:
+    //    128 x 96 tiles, 32-deep k-tiles, 4 waves of 32 x 96, two workgroups
+    //    per CU.  A wide tile's round is all or nothing: 1.1 rounds cost two
+    //    (FFN up at 9,216 rows: 145.8 us on 256 x 192, 101.8 on 128 x 96; QKV
+    //    at 12,288: 142.0 against 94.1), and a padded batch whose real rows
+    //    fill three quarters of one round still takes the whole round (FFN up
+    //    at 6,124 of 8,192 rows: 80.1 against 66.0 us).  The wide tiles are
+    //    ahead only on a round filled exactly (FFN up at 8,192 dense rows:
+    //    83.8 against 88.1 us);
     //  * wide outputs over a short K with many tiles per CU: 32-deep k-tiles,
     //    two workgroups per CU, so one workgroup's GELU epilogue runs beside
     //    the other's MFMAs;
@@ -1731,12 +1751,14 @@ hipError_t launch_gemm_f32(const GemmArgs& a, int epi, hipStream_t s) {
         return launch_persistent<64, 64, 64, 2, 2, 2>(a, epi, s, 2);
     if (ok && S > 1 && a.K % (32 * S) == 0)    // mid-size split products
         return launch_persistent<128, 128, 32, 2, 2, 2>(a, epi, s, 2);
-    if (ok && S == 1 && a.N % 256 == 0 && a.K % 32 == 0 &&
-        (int64_t)((a.M_max + 255) / 256) * (a.N / 256) >= (int64_t)cu_count())
-        return launch_persistent<256, 256, 32, 2, 4, 2>(a, epi, s, 1);
-    if (ok && S == 1 && a.N % 192 == 0 && a.K % 32 == 0 &&
-        (int64_t)((a.M_max + 255) / 256) * (a.N / 192) >= (int64_t)cu_count())
-        return launch_persistent<256, 192, 32, 4, 2, 2>(a, epi, s, 1);
+    const int64_t rows256 = (a.M_max + 255) / 256, cus = cu_count();
+    const bool wide256 = ok && S == 1 && a.N % 256 == 0 && a.K % 32 == 0 && rows256 * (a.N / 256) >= cus;
+    const bool wide192 = ok && S == 1 && a.N % 192 == 0 && a.K % 32 == 0 && rows256 * (a.N / 192) >= cus;
+    if (ok && S == 1 && a.N % 96 == 0 && a.K % 32 == 0 &&
+        ((wide256 && rows256 * (a.N / 256) < 2 * cus) || (!wide256 && wide192 && rows256 * (a.N / 192) < 2 * cus)))
+        return launch_persistent<128, 96, 32, 4, 1, 2>(a, epi, s, 2);
+    if (wide256) return launch_persistent<256, 256, 32, 2, 4, 2>(a, epi, s, 1);
+    if (wide192) return launch_persistent<256, 192, 32, 4, 2, 2>(a, epi, s, 1);
     if (ok && a.K % 32 == 0 && a.N >= 1536 && a.K < 1024 && tiles128 >= 8 * (int64_t)cu_count() && S == 1)
         return launch_persistent<128, 128, 32, 2, 2, 2>(a, epi, s, 2);
     if (ok && a.K % (64 * S) == 0)
