@@ -87,7 +87,7 @@ _SIGS = {
                                           _f32, _vp]),
     "ebh_op_add_layer_norm_y16": (_i32, [_vp, _vp, _vp, _vp, _vp, _i32, _i32, _f32, _vp]),
     "ebh_op_add_layer_norm_b16": (_i32, [_vp, _vp, _vp, _vp, _vp, _i32, _i32, _f32, _vp]),
-    "ebh_op_pool": (_i32, [_vp, _vp, _i32, _i32, _i32, _i32, _vp, _vp]),
+    "ebh_op_pool": (_i32, [_vp, _vp, _i32, _i32, _i32, _i32, _vp, _vp, _vp]),
     "ebh_op_pool_b16": (_i32, [_vp, _vp, _i32, _i32, _i32, _i32, _vp, _vp]),
     "ebh_op_pack": (_i32, [_vp, _vp, _i32, _i32, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
     "ebh_op_embed_ln": (_i32, [_vp, _vp, _vp, _i32, _vp, _vp, _vp, _vp, _vp, _i32, _i32, _f32,

@@ -542,7 +542,7 @@ int enqueue_kernels(ebh_model* m, Workspace& w, const int* d_ids, const int* d_m
     }
     prof_begin(m, prof_kind, EBH_PROF_POOL, s, pp, on);
     HIP_TRY(bf16 ? ebh::launch_pool_b16(w.X16, w.cu, B, H, S, normalize, d_out, s)
-                 : ebh::launch_pool(w.X, w.cu, B, H, S, normalize, d_out, s));
+                 : ebh::launch_pool(w.X, w.cu, B, H, S, normalize, w.Y, d_out, s));
     prof_end(m, s, pp, on);
     if (d_scores) HIP_TRY(ebh::launch_cls_head(d_out, m->cls_w, m->cls_b, B, H, d_scores, s));
     return EBH_OK;
@@ -1465,10 +1465,13 @@ int ebh_op_add_layer_norm_b16(const uint16_t* y, const float* bias, uint16_t* x1
 }
 
 int ebh_op_pool(const float* x, const int32_t* cu_seqlens, int32_t B, int32_t H, int32_t S,
-                int32_t normalize, float* out, void* stream) {
+                int32_t normalize, float* partials, float* out, void* stream) {
     if (!x || !cu_seqlens || !out) return fail(EBH_ERR_INVALID_ARG, "null buffer");
     if (B < 0 || H <= 0 || H > 2048 || S < 0) return fail(EBH_ERR_INVALID_ARG, "bad pool shape");
-    HIP_TRY(ebh::launch_pool(x, cu_seqlens, B, H, S, normalize ? 1 : 0, out,
+    auto al16 = [](const void* p) { return ((uintptr_t)p & 15) == 0; };
+    if (ebh::pool_partials_floats(B, H, S) > 0 && al16(x) && al16(out) && (!partials || !al16(partials)))
+        return fail(EBH_ERR_INVALID_ARG, "partials: null or not 16-byte aligned");
+    HIP_TRY(ebh::launch_pool(x, cu_seqlens, B, H, S, normalize ? 1 : 0, partials, out,
                              static_cast<hipStream_t>(stream)));
     return EBH_OK;
 }

@@ -160,8 +160,12 @@ hipError_t launch_embed_ln(const int* tok_id, const int* tok_pos, const int* n_t
                            int* err, uint16_t* x16, hipStream_t s);
 
 // Masked mean over each packed sequence, optional L2 normalisation; out [B, H].
+// Floats of `partials` the fp32 pool needs: B * ceil(S / 32) * H when it
+// sums fewer sequences than CUs, of more than 32 positions and H % 4 == 0,
+// H <= 768, in 32-row chunks; else 0 (unused).
+int64_t pool_partials_floats(int B, int H, int S);
 hipError_t launch_pool(const float* x, const int* cu_seqlens, int B, int H, int S,
-                       int normalize, float* out, hipStream_t s);
+                       int normalize, float* partials, float* out, hipStream_t s);
 // The same over a bf16 residual stream x16 (sums in fp32).
 hipError_t launch_pool_b16(const uint16_t* x16, const int* cu_seqlens, int B, int H, int S,
                            int normalize, float* out, hipStream_t s);

@@ -813,16 +813,136 @@ hipError_t launch_pack_embed_few(const int* ids, const int* mask, int B, int S, 
 }
 
 // ---------------------------------------------------------------------------
-// mean_pool (src/lib.rs:993-1010) + normalise (src/lib.rs:605-612): one
-// 512-thread workgroup per sequence.  Wave w sums tokens w, w+8, w+16, ...
-// with four rows in flight per step (the sum is latency-bound otherwise);
-// wave 0 then adds the eight partial rows in wave order, divides by
-// max(count, 1) and optionally scales by 1 / max(||x||, 1e-12).  The order
-// of additions depends only on the sequence's own length, so a sequence gives
-// the same vector wherever it sits in the batch.  A sequence with no real
-// token among S > 0 positions is NaN, as the reference's all -inf softmax row
-// makes it.
+// mean_pool (src/lib.rs:993-1010) + normalise (src/lib.rs:605-612).
+//
+// One 512-thread workgroup per sequence (pool_kernel): wave w sums tokens w,
+// w+8, w+16, ... with four rows in flight per step (the sum is latency-bound
+// otherwise); wave 0 then adds the eight partial rows in wave order, divides
+// by max(count, 1) and optionally scales by 1 / max(||x||, 1e-12).
+//
+// Fewer sequences than CUs, of more than POOL_CR positions, with rows of
+// H % 4 == 0 floats, H <= 768 (MiniLM, BERT-base): one sequence per
+// workgroup would leave most CUs idle while each waits a dozen dependent
+// memory round trips (16 sequences of 256-512 tokens: 18.0 us).  There the
+// tokens are summed in chunks of POOL_CR rows, a workgroup per chunk
+// (pool_chunk_kernel): thread t of 768 owns float4 column t % F of the row
+// (F = H / 4) and sums rows r0 + g, r0 + g + RG, ... of the chunk (g = t / F,
+// RG = 768 / F >= 4 row groups), all loaded before the first add; the RG
+// sums are added in g order into `part` [B, C, H] (C = ceil(S / POOL_CR)),
+// and pool_finish_kernel adds a sequence's chunks in order and finishes as
+// above (c4: 18.0 -> ~8 us).
+//
+// Either way the order of additions depends only on the sequence's own
+// length and the batch's shape, so a sequence gives the same vector wherever
+// it sits in the batch.  A sequence with no real token among S > 0 positions
+// is NaN, as the reference's all -inf softmax row makes it.
 // ---------------------------------------------------------------------------
+constexpr int POOL_CR = 32;    // rows per chunk
+constexpr int POOL_NT = 768;   // threads per chunk workgroup: whole rows of float4 for H = 384 and 768
+
+// Divide by the count, then the optional L2 normalisation, for the float4
+// column t < F of sequence b (v = its sum); every thread of the workgroup
+// takes part (the norm is a workgroup sum, over waves in order).
+__device__ __forceinline__ void pool_finish_row(float4 v, int t, int F, int len, int S, int normalize,
+                                                float* __restrict__ out_row, float* wsum) {
+    const float count = fmaxf((float)len, 1.0f);
+    const bool all_masked = (len == 0 && S > 0);
+    v.x = v.x / count; v.y = v.y / count; v.z = v.z / count; v.w = v.w / count;
+    if (all_masked) v = make_float4(__builtin_nanf(""), __builtin_nanf(""), __builtin_nanf(""), __builtin_nanf(""));
+    float ss = t < F ? (v.x * v.x + v.y * v.y) + (v.z * v.z + v.w * v.w) : 0.0f;
+    ss = wave_sum(ss);
+    const int nw = (int)(blockDim.x >> 6);
+    if ((t & 63) == 0) wsum[t >> 6] = ss;
+    __syncthreads();
+    float tot = wsum[0];
+    for (int w = 1; w < nw; ++w) tot += wsum[w];
+    if (t < F) {
+        if (normalize) {
+            const float norm = fmaxf(sqrtf(tot), 1e-12f);
+            v.x = v.x / norm; v.y = v.y / norm; v.z = v.z / norm; v.w = v.w / norm;
+        }
+        reinterpret_cast<float4*>(out_row)[t] = v;
+    }
+}
+
+// This thread's rows r0 + g, r0 + g + RG, ... below r1 (<= r0 + POOL_CR;
+// U >= POOL_CR / RG of them), and their sum in that order from 0.
+template <int U>
+__device__ __forceinline__ void pool_load(float4 (&v)[U], const float4* __restrict__ xp, int F, int RG, int g,
+                                          int r0, int r1) {
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+        const int r = r0 + g + u * RG;
+        v[u] = r < r1 ? xp[(int64_t)r * F] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    }
+}
+template <int U>
+__device__ __forceinline__ float4 pool_add(const float4 (&v)[U], int RG, int g, int r0, int r1) {
+    float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+        if (r0 + g + u * RG < r1) {
+            acc.x += v[u].x; acc.y += v[u].y; acc.z += v[u].z; acc.w += v[u].w;
+        }
+    return acc;
+}
+
+// The chunk's sum for float4 column t < F: the row groups' sums in g order.
+__device__ __forceinline__ float4 pool_groups(const float4* red, int F, int RG, int t) {
+    float4 sum = red[t];
+    for (int q = 1; q < RG; ++q) {
+        const float4 o = red[q * F + t];
+        sum.x += o.x; sum.y += o.y; sum.z += o.z; sum.w += o.w;
+    }
+    return sum;
+}
+
+// One chunk of one sequence: grid (C, B), POOL_NT threads, RG >= POOL_CR / U.
+template <int U>
+__global__ __launch_bounds__(POOL_NT) void pool_chunk_kernel(const float* __restrict__ x, const int* __restrict__ cu,
+                                                             int H, int C, float* __restrict__ part) {
+    __shared__ float4 red[POOL_NT];
+    const int F = H >> 2, RG = POOL_NT / F;
+    const int b = blockIdx.y, ch = blockIdx.x, t = threadIdx.x;
+    const int start = cu[b], len = cu[b + 1] - start, r0 = ch * POOL_CR;
+    if (r0 >= len) return;   // past the sequence: the finish step skips this chunk
+    const int col = t % F, g = t / F;
+    const float4* xp = reinterpret_cast<const float4*>(x + (int64_t)start * H) + col;
+    const int r1 = g < RG ? min(len, r0 + POOL_CR) : r0;   // idle threads: no rows
+    float4 v[U];
+    pool_load<U>(v, xp, F, RG, g, r0, r1);
+    red[t] = pool_add<U>(v, RG, g, r0, r1);
+    __syncthreads();
+    if (t < F) reinterpret_cast<float4*>(part + ((int64_t)b * C + ch) * H)[t] = pool_groups(red, F, RG, t);
+}
+
+// A sequence's chunk sums added in chunk order, then finished: grid B,
+// F rounded up to whole waves.
+__global__ __launch_bounds__(POOL_NT) void pool_finish_kernel(const float* __restrict__ part,
+                                                              const int* __restrict__ cu, int H, int S,
+                                                              int normalize, int C, float* __restrict__ out) {
+    __shared__ float wsum[POOL_NT / 64];
+    const int F = H >> 2, b = blockIdx.x, t = threadIdx.x;
+    const int len = cu[b + 1] - cu[b], nch = (len + POOL_CR - 1) / POOL_CR;
+    float4 v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    if (t < F && nch > 0) {
+        const float4* pp = reinterpret_cast<const float4*>(part + (int64_t)b * C * H) + t;
+        v = pp[0];
+        constexpr int U = 8;
+        for (int c0 = 1; c0 < nch; c0 += U) {
+            float4 q[U];
+#pragma unroll
+            for (int u = 0; u < U; ++u)
+                q[u] = c0 + u < nch ? pp[(int64_t)(c0 + u) * F] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+#pragma unroll
+            for (int u = 0; u < U; ++u)
+                if (c0 + u < nch) {
+                    v.x += q[u].x; v.y += q[u].y; v.z += q[u].z; v.w += q[u].w;
+                }
+        }
+    }
+    pool_finish_row(v, t, F, len, S, normalize, out + (int64_t)b * H, wsum);
+}
 constexpr int POOL_WAVES = 8;
 
 template <int NC>
@@ -890,9 +1010,29 @@ __global__ __launch_bounds__(64 * POOL_WAVES) void pool_kernel(const float* __re
     }
 }
 
+// Chunks per sequence of the chunked path, 0 where pool_kernel runs: H % 4
+// == 0 and at least 4 row groups (H <= 768), so a thread's rows of a chunk
+// take at most 8 loads; fewer sequences than CUs, more than one chunk.
+static int pool_chunks(int B, int H, int S) {
+    const int C = (S + POOL_CR - 1) / POOL_CR;
+    return H % 4 == 0 && H / 4 <= POOL_NT / 4 && C > 1 && B < device_cu_count() ? C : 0;
+}
+
+int64_t pool_partials_floats(int B, int H, int S) { return (int64_t)B * pool_chunks(B, H, S) * H; }
+
 hipError_t launch_pool(const float* x, const int* cu_seqlens, int B, int H, int S, int normalize,
-                       float* out, hipStream_t s) {
+                       float* partials, float* out, hipStream_t s) {
     if (B <= 0) return hipSuccess;
+    const int C = pool_chunks(B, H, S);
+    if (C > 0 && al16(x) && al16(out)) {
+        const bool u4 = POOL_NT / (H / 4) >= POOL_CR / 4;   // 8 or more row groups: 4 rows each
+        if (!partials || !al16(partials)) return hipErrorInvalidValue;
+        if (u4) hipLaunchKernelGGL(pool_chunk_kernel<4>, dim3(C, B), dim3(POOL_NT), 0, s, x, cu_seqlens, H, C, partials);
+        else hipLaunchKernelGGL(pool_chunk_kernel<8>, dim3(C, B), dim3(POOL_NT), 0, s, x, cu_seqlens, H, C, partials);
+        hipLaunchKernelGGL(pool_finish_kernel, dim3(B), dim3((H / 4 + 63) / 64 * 64), 0, s, partials,
+                           cu_seqlens, H, S, normalize, C, out);
+        return hipGetLastError();
+    }
     const int nc = (H + 63) / 64;
     const dim3 grid(B), block(64 * POOL_WAVES);
     if (nc <= 4) hipLaunchKernelGGL(pool_kernel<4>, grid, block, 0, s, x, cu_seqlens, H, S, normalize, out);

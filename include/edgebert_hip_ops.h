@@ -108,9 +108,13 @@ EBH_API int ebh_op_add_layer_norm_b16(const uint16_t* y, const float* bias, uint
 
 /* mean_pool (src/lib.rs:993-1010) over packed sequences (+ the normalise tail,
  * src/lib.rs:605-612, when normalize != 0); S is the padded length the caller
- * had (S > 0 and an empty sequence gives NaN, as in the reference). */
+ * had (S > 0 and an empty sequence gives NaN, as in the reference).  With
+ * H % 4 == 0, H <= 768, x and out 16-byte aligned, S > 32 and fewer
+ * sequences than the device has CUs, each sequence's 32-row chunks are summed
+ * by workgroups of their own into `partials`: B * ceil(S / 32) * H floats,
+ * 16-byte aligned (otherwise unused, and may be null). */
 EBH_API int ebh_op_pool(const float* x, const int32_t* cu_seqlens, int32_t B, int32_t H, int32_t S,
-                int32_t normalize, float* out, void* stream);
+                int32_t normalize, float* partials, float* out, void* stream);
 /* The same over a bf16 residual stream x16 [T, H] (bf16 bits, 8-byte aligned,
  * H % 4 == 0); sums in fp32. */
 EBH_API int ebh_op_pool_b16(const uint16_t* x16, const int32_t* cu_seqlens, int32_t B, int32_t H, int32_t S,

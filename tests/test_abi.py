@@ -150,7 +150,9 @@ def test_op_entry_points_validate_before_launch(L):
     assert L.ebh_op_layer_norm(p, p, p, 1, 4096, 1e-12, p, nul) == N.EBH_ERR_INVALID_ARG
     assert L.ebh_op_add_layer_norm(p, nul, p, p, p, 1, 64, 1e-12, nul) == N.EBH_ERR_INVALID_ARG
     assert L.ebh_op_gemm(p, 4, p, 4, 0, nul, nul, 0, p, 4, 1, 4, 4, 0, nul) == N.EBH_ERR_INVALID_ARG  # bias needed
-    assert L.ebh_op_pool(p, p, -1, 64, 4, 1, p, nul) == N.EBH_ERR_INVALID_ARG
+    assert L.ebh_op_pool(p, p, -1, 64, 4, 1, p, p, nul) == N.EBH_ERR_INVALID_ARG
+    if buf.ctypes.data % 16 == 0:   # S > 32: the chunk sums need a partials buffer
+        assert L.ebh_op_pool(p, p, 1, 64, 64, 1, nul, p, nul) == N.EBH_ERR_INVALID_ARG
     assert L.ebh_op_pack(p, p, -1, 4, p, p, p, p, p, p, nul) == N.EBH_ERR_INVALID_ARG
     assert L.ebh_op_f32_to_bf16(p, p, -1, nul) == N.EBH_ERR_INVALID_ARG
 

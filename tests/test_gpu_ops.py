@@ -655,19 +655,35 @@ def test_pool_bf16(env, normalize):
         np.testing.assert_allclose(got[bi], want, rtol=0, atol=2e-6)
 
 
-@pytest.mark.parametrize("normalize", [0, 1])
-def test_pool(env, normalize):
-    torch, eb, Nn, L = env
-    H, S = 384, 64
-    lengths = [1, 5, 64, 0, 33]
+def run_pool(torch, Nn, L, x, lengths, H, S, normalize):
     cu = np.concatenate([[0], np.cumsum(lengths)]).astype(np.int32)
-    x = np.random.default_rng(1).standard_normal((cu[-1], H)).astype(np.float32)
-    dout = torch.empty((len(lengths), H), device="cuda")
+    dout = torch.full((len(lengths), H), float("nan"), device="cuda")
+    part = torch.full((len(lengths) * max(1, -(-S // 32)) * H,), float("nan"), device="cuda")
     dx, dcu = dev(torch, x), dev(torch, cu)
-    Nn.check(L.ebh_op_pool(vp(dx), vp(dcu), len(lengths), H, S, normalize,
+    Nn.check(L.ebh_op_pool(vp(dx), vp(dcu), len(lengths), H, S, normalize, vp(part),
                            vp(dout), stream(torch)))
     torch.cuda.synchronize()
-    got = dout.cpu().numpy()
+    return dout.cpu().numpy(), cu
+
+
+@pytest.mark.parametrize("normalize", [0, 1])
+@pytest.mark.parametrize("H,S,lengths", [
+    (384, 64, [1, 5, 64, 0, 33]),                       # two 32-row chunks
+    (384, 32, [1, 32, 0, 17]),                          # one chunk: one workgroup per sequence
+    (384, 512, [512, 1, 33, 0, 300, 32, 64, 65, 511]),  # up to 16 chunks (c4's lengths)
+    (768, 512, [512, 100, 31, 0, 257]),                 # BERT-base width: 4 row groups, 8 rows each
+    (100, 96, [96, 7, 0, 50]),                          # 25 float4 columns, 30 row groups, idle threads
+    (1024, 128, [128, 3, 0, 97]),                       # H > 768: one workgroup per sequence
+    (90, 64, [64, 1, 0, 40]),                           # H % 4 != 0: the same
+])
+def test_pool(env, normalize, H, S, lengths):
+    """mean_pool + normalise against float64: a few sequences, so those of
+    more than 32 positions, H % 4 == 0 and H <= 768 are summed by a workgroup
+    per 32-row chunk."""
+    torch, eb, Nn, L = env
+    cu = np.concatenate([[0], np.cumsum(lengths)]).astype(np.int32)
+    x = np.random.default_rng(H + S).standard_normal((max(cu[-1], 1), H)).astype(np.float32)
+    got, cu = run_pool(torch, Nn, L, x, lengths, H, S, normalize)
     for b, n in enumerate(lengths):
         if n == 0:
             assert np.isnan(got[b]).all()            # all-masked sequence: NaN, as the reference
@@ -676,6 +692,27 @@ def test_pool(env, normalize):
         if normalize:
             want = want / max(np.linalg.norm(want), 1e-12)
         np.testing.assert_allclose(got[b], want, rtol=0, atol=2e-6)
+
+
+def test_pool_order_depends_on_the_sequence_only(env):
+    """A sequence's vector is the same bits wherever it sits in the batch and
+    whatever padded length S the batch has (chunks past its end are skipped),
+    on the chunked path and on the one-workgroup-per-sequence path (a batch of
+    more sequences than CUs)."""
+    torch, eb, Nn, L = env
+    H = 384
+    rng = np.random.default_rng(9)
+    seqs = [rng.standard_normal((n, H)).astype(np.float32) for n in (300, 33, 512, 1)]
+    a, _ = run_pool(torch, Nn, L, np.concatenate(seqs), [len(q) for q in seqs], H, 512, 1)
+    order = [3, 1, 0, 2]
+    b, _ = run_pool(torch, Nn, L, np.concatenate([seqs[i] for i in order]), [len(seqs[i]) for i in order],
+                    H, 1024, 1)
+    np.testing.assert_array_equal(b, a[order])
+    many = [seqs[i % 4] for i in range(320)]
+    c, _ = run_pool(torch, Nn, L, np.concatenate(many), [len(q) for q in many], H, 512, 1)
+    for i in range(4):
+        np.testing.assert_array_equal(c[i::4], np.broadcast_to(c[i], c[i::4].shape))
+        np.testing.assert_allclose(c[i], a[i], rtol=0, atol=2e-7)
 
 
 def test_pack_with_holes(env):
