@@ -334,15 +334,19 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_persistent_kernel
     const int S = p.splits > 1 ? p.splits : 1;
     const int nwork = ntiles * S;
     const int nk = p.K / BK / S;                  // k-tiles per work item
-    // Workgroup b runs on XCD b % 8.  Each XCD takes an eighth of the work
-    // items as one consecutive range (N-fastest tiles, which share A row
-    // panels in that XCD's L2), and its G / 8 workgroups walk the range in
-    // steps of G / 8.  When the items are not a multiple of G, every XCD's
-    // range ends in a partial step, so the last step's items spread over all
-    // XCDs instead of filling the first ones twice.
+    // Workgroup b runs on XCD b % 8, and each XCD's workgroups take
+    // consecutive N-fastest tiles, which share A row panels in that XCD's L2.
+    // Whole rounds of items: workgroup x * G / 8 + b / 8 of XCD x walks items
+    // in steps of G (each round's 32 consecutive tiles per XCD).  Otherwise
+    // each XCD takes an eighth of the items as one consecutive range, walked
+    // in steps of G / 8, so that the last, partial step spreads over all XCDs
+    // (fewer items than workgroups had left whole XCDs idle: c2 QKV 32.7 ->
+    // 31.2 us).
     const int G = gridDim.x;
     int u0 = blockIdx.x, ustep = G, uend = nwork;
-    if ((G & 7) == 0) {
+    if ((G & 7) == 0 && nwork % G == 0) {
+        u0 = (blockIdx.x & 7) * (G >> 3) + (blockIdx.x >> 3);
+    } else if ((G & 7) == 0) {
         const int x = blockIdx.x & 7;
         ustep = G >> 3;
         u0 = (int)((int64_t)x * nwork / 8) + (blockIdx.x >> 3);

@@ -118,9 +118,99 @@ __global__ __launch_bounds__(256) void pack_scatter_kernel(const int* __restrict
     }
 }
 
+// The whole packing in one 1024-thread workgroup, for batches of at most
+// PACK1_MAX_POS positions and PACK1_MAX_B sequences (c2, c4: three launches
+// made one).  Positions go in rounds of 1024 in order: each round's mask
+// flags are ranked by a ballot per wave and the waves' counts added in wave
+// order, so every kept token lands where the three-kernel path puts it.  The
+// thread holding position b * S records cu[b], the tokens before it.  The
+// order of the sequences by decreasing length is the same counting sort as
+// in pack_scan_kernel, over counts held in LDS.
+constexpr int PACK1_MAX_POS = 16384, PACK1_MAX_B = 1024;
+__global__ __launch_bounds__(1024) void pack_one_kernel(const int* __restrict__ ids, const int* __restrict__ mask,
+                                                        int B, int S, int* __restrict__ counts,
+                                                        int* __restrict__ cu, int* __restrict__ n_tokens,
+                                                        int* __restrict__ tok_id, int* __restrict__ tok_pos,
+                                                        int* __restrict__ order) {
+    __shared__ int wcount[16];
+    __shared__ int cu_s[PACK1_MAX_B + 1];
+    __shared__ int next[ORDER_BINS];
+    __shared__ int buf[1024];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int P = B * S;
+    constexpr int R = PACK1_MAX_POS / 1024;
+    int mv[R], iv[R];   // every round's mask and id, loaded before the first ranking
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        const int p = r * 1024 + tid;
+        mv[r] = p < P ? mask[p] : 0;
+        iv[r] = p < P ? ids[p] : 0;
+    }
+    for (int b = tid; b <= B; b += 1024) cu_s[b] = 0;   // S == 0: every sequence empty
+    __syncthreads();
+    int base = 0;
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        if (r * 1024 >= P) break;   // uniform
+        const int p = r * 1024 + tid;
+        const bool on = mv[r] != 0;
+        const int id = iv[r];
+        const unsigned long long bal = __ballot(on);
+        if (lane == 0) wcount[wave] = __popcll(bal);
+        __syncthreads();
+        // Lane w < 16 holds wave w's count: the waves before this one, and all.
+        const int c = lane < 16 ? wcount[lane] : 0;
+        int before = lane < wave ? c : 0, total = c;
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) {   // whole-wave sums: every lane needs them
+            before += __shfl_xor(before, o);
+            total += __shfl_xor(total, o);
+        }
+        const unsigned long long below = lane ? (bal & ((~0ull) >> (64 - lane))) : 0ull;
+        const int dst = base + before + __popcll(below);
+        if (p < P && p % S == 0) cu_s[p / S] = dst;
+        if (on) {
+            tok_id[dst] = id;
+            tok_pos[dst] = p % S;
+        }
+        base += total;
+        __syncthreads();   // wcount is rewritten next round
+    }
+    if (tid == 0) {
+        cu_s[B] = base;
+        *n_tokens = base;
+    }
+    __syncthreads();
+    for (int b = tid; b <= B; b += 1024) cu[b] = cu_s[b];
+    for (int b = tid; b < B; b += 1024) counts[b] = cu_s[b + 1] - cu_s[b];
+    if (!order) return;   // uniform over the workgroup
+    next[tid] = 0;
+    __syncthreads();
+    for (int b = tid; b < B; b += 1024) atomicAdd(&next[min(cu_s[b + 1] - cu_s[b], ORDER_BINS - 1)], 1);
+    __syncthreads();
+    const int n_bin = next[ORDER_BINS - 1 - tid];
+    buf[tid] = n_bin;
+    __syncthreads();
+    for (int off = 1; off < 1024; off <<= 1) {
+        const int v = tid >= off ? buf[tid - off] : 0;
+        __syncthreads();
+        buf[tid] += v;
+        __syncthreads();
+    }
+    next[ORDER_BINS - 1 - tid] = buf[tid] - n_bin;
+    __syncthreads();
+    for (int b = tid; b < B; b += 1024)
+        order[atomicAdd(&next[min(cu_s[b + 1] - cu_s[b], ORDER_BINS - 1)], 1)] = b;
+}
+
 hipError_t launch_pack(const int* ids, const int* mask, int B, int S, int* counts, int* cu,
                        int* n_tokens, int* tok_id, int* tok_pos, hipStream_t s, int* order) {
     if (B <= 0) return hipSuccess;
+    if (B <= PACK1_MAX_B && (int64_t)B * S <= PACK1_MAX_POS) {
+        hipLaunchKernelGGL(pack_one_kernel, dim3(1), dim3(1024), 0, s, ids, mask, B, S, counts, cu, n_tokens,
+                           tok_id, tok_pos, order);
+        return hipGetLastError();
+    }
     hipLaunchKernelGGL(pack_count_kernel, dim3(B), dim3(256), 0, s, mask, S, counts);
     hipLaunchKernelGGL(pack_scan_kernel, dim3(1), dim3(1024), 0, s, counts, B, cu, n_tokens, order);
     hipLaunchKernelGGL(pack_scatter_kernel, dim3(B), dim3(256), 0, s, ids, mask, S, cu, tok_id,

@@ -715,15 +715,21 @@ def test_pool_order_depends_on_the_sequence_only(env):
         np.testing.assert_allclose(c[i], a[i], rtol=0, atol=2e-7)
 
 
-def test_pack_with_holes(env):
+@pytest.mark.parametrize("B,S", [
+    (37, 300),     # 11,100 positions: the one-workgroup packing
+    (16, 1024),    # 16,384: its largest batch
+    (1, 1),
+    (1025, 16),    # more sequences than it takes: count, scan and scatter kernels
+    (100, 200),    # 20,000 positions: the same
+])
+def test_pack_with_holes(env, B, S):
     """Masks need not be a prefix: every mask==1 token is kept with its position."""
     torch, eb, Nn, L = env
-    rng = np.random.default_rng(5)
-    B, S = 37, 300
+    rng = np.random.default_rng(5 + B + S)
     ids = rng.integers(0, 30522, (B, S)).astype(np.int32)
     mask = (rng.random((B, S)) < 0.6).astype(np.int32)
-    mask[3] = 0
-    mask[4] = 1
+    mask[3 % B] = 0
+    mask[4 % B] = 1
     d = {k: torch.zeros(n, dtype=torch.int32, device="cuda")
          for k, n in [("counts", B), ("cu", B + 1), ("n", 1), ("tid", B * S), ("tpos", B * S), ("err", 1)]}
     d["err"].fill_(7)
@@ -737,6 +743,7 @@ def test_pack_with_holes(env):
     np.testing.assert_array_equal(d["tid"].cpu().numpy()[:n], ids[mask != 0])
     np.testing.assert_array_equal(d["tpos"].cpu().numpy()[:n], np.nonzero(mask)[1])
     np.testing.assert_array_equal(d["cu"].cpu().numpy(), np.concatenate([[0], np.cumsum(mask.sum(1))]))
+    np.testing.assert_array_equal(d["counts"].cpu().numpy(), mask.sum(1))
     assert int(d["err"].item()) == 0
 
 
