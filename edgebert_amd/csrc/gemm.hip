@@ -1754,8 +1754,8 @@ hipError_t launch_gemm_f32(const GemmArgs& a, int epi, hipStream_t s) {
     const int64_t tiles128 = (int64_t)((a.M_max + 127) / 128) * ((a.N + 127) / 128);
     if (ok && a.K % (64 * S) == 0 && 2 * tiles128 < (int64_t)cu_count())
         return launch_persistent<64, 64, 64, 2, 2, 2>(a, epi, s, 2);
-    if (ok && S > 1 && a.K % (32 * S) == 0 && a.N % 96 == 0)   // mid-size split products
-        return launch_persistent<128, 96, 32, 4, 1, 2>(a, epi, s, 2);
+    if (ok && S > 1 && a.K % (32 * S) == 0 && a.N % 96 == 0 && tiles128 < (int64_t)cu_count())
+        return launch_persistent<128, 96, 32, 4, 1, 2>(a, epi, s, 2);   // mid-size split products (mid_splits)
     if (ok && S > 1 && a.K % (32 * S) == 0)
         return launch_persistent<128, 128, 32, 2, 2, 2>(a, epi, s, 2);
     const int64_t rows256 = (a.M_max + 255) / 256, cus = cu_count();
@@ -1794,14 +1794,19 @@ int gemm_f32_splits(int M_max, int N, int K) {
 
 // Mid-size products (half to two 128 x 128 tiles per CU, e.g. 16 long
 // sentences): two workgroups per CU, split over K.
-//  * N whole 96-column panels (MiniLM's 384): 128 x 96 tiles, as many splits
-//    (4, 3 or 2) as keep at least six 32-deep k-tiles per work item and at
-//    most two rounds of workgroups by M_max.  Measured at 6,124 of 8,192
-//    tokens: FFN down 69.2 us (128 x 128, 3 splits) -> 62.0 us (4 splits);
-//    the attention-output projection takes 2 splits, 27.0 us, and its
-//    LayerNorm then sums two partials instead of three (c4 9.3k -> 9.6k
-//    sentences/s).  With 4 splits it took 24.8 us, but the LayerNorm's two
-//    extra partial reads cost as much.
+//  * N whole 96-column panels (MiniLM's 384) and fewer 128 x 128 tiles than
+//    CUs: 128 x 96 tiles, as many splits (4, 3 or 2) as keep at least six
+//    32-deep k-tiles per work item and at most two rounds of workgroups by
+//    M_max.  Measured at 6,124 of 8,192 tokens: FFN down 69.2 us (128 x 128,
+//    3 splits) -> 62.0 us (4 splits); the attention-output projection takes 2
+//    splits, 27.0 us, and its LayerNorm then sums two partials instead of
+//    three (c4 9.3k -> 9.6k sentences/s).  With 4 splits it took 24.8 us, but
+//    the LayerNorm's two extra partial reads cost as much.  At 8,192 dense
+//    tokens: out 42.1 -> 27.9 us, FFN down 127.6 -> 79.8 us.  With more
+//    128 x 128 tiles (16,384 padded positions) a ragged batch's items came to
+//    just over one round (8,585 tokens: 544 items for 512 workgroups), slower
+//    than the unsplit product (FFN down 99.8 -> 112.1 us), so those keep the
+//    rule below;
 //  * otherwise 128 x 128 tiles, split so that the work items come to about
 //    one round of workgroups (counted by M_max, which includes padding).
 //    Measured at 6.1k of 8k tokens, FFN down: 103.6 us unsplit, 72.0 us in
@@ -1810,7 +1815,7 @@ static int mid_splits(int M_max, int N, int K) {
     const int64_t tiles128 = (int64_t)((M_max + 127) / 128) * ((N + 127) / 128);
     const int64_t slots = 2 * (int64_t)cu_count();
     if (2 * tiles128 < (int64_t)cu_count() || tiles128 >= slots) return 1;
-    if (N % 96 == 0) {
+    if (N % 96 == 0 && tiles128 < (int64_t)cu_count()) {
         const int64_t tiles96 = (int64_t)((M_max + 127) / 128) * (N / 96);
         for (int S : {4, 3, 2})
             if (K % (32 * S) == 0 && K / S >= 192 && tiles96 * S <= 2 * slots) return S;
