@@ -34,60 +34,81 @@ __global__ __launch_bounds__(256) void pack_count_kernel(const int* __restrict__
     if (tid == 0) counts[b] = part[0] + part[1] + part[2] + part[3];
 }
 
+constexpr int ORDER_BINS = 1024;   // length bins of the longest-first order
+
+// Exclusive prefix sum over the 1024 threads of a workgroup (thread order),
+// and the total: an inclusive scan within each wave by lane shuffles, then
+// the waves' totals added in wave order.  Two barriers; `wsum` holds 16 ints
+// of LDS.  Every thread of the workgroup must call it.
+__device__ __forceinline__ int block_excl_scan_1024(int v, int* wsum, int& total) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    int incl = v;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const int y = __shfl_up(incl, o);
+        if (lane >= o) incl += y;
+    }
+    if (lane == 63) wsum[wave] = incl;
+    __syncthreads();
+    int before = 0, tot = 0;
+#pragma unroll
+    for (int w = 0; w < 16; ++w) {
+        const int c = wsum[w];
+        before += w < wave ? c : 0;
+        tot += c;
+    }
+    __syncthreads();   // wsum may be reused
+    total = tot;
+    return before + incl - v;
+}
+
+// order[0..B): the sequences by decreasing length (counts, clamped to
+// ORDER_BINS - 1; ties in any order), a counting sort by the 1024 threads of
+// one workgroup.  Thread t takes bin 1023 - t, so the scan runs from the
+// longest length down and a bin's exclusive value is its first slot.
+__device__ __forceinline__ void order_by_length(const int* counts, int B, int* next, int* wsum,
+                                                int* __restrict__ order) {
+    static_assert(ORDER_BINS == 1024, "one bin per thread");
+    const int tid = threadIdx.x;
+    next[tid] = 0;
+    __syncthreads();
+    for (int b = tid; b < B; b += 1024) atomicAdd(&next[min(counts[b], ORDER_BINS - 1)], 1);
+    __syncthreads();
+    int total;
+    const int first = block_excl_scan_1024(next[ORDER_BINS - 1 - tid], wsum, total);
+    next[ORDER_BINS - 1 - tid] = first;   // each thread rewrites only its own bin
+    __syncthreads();
+    for (int b = tid; b < B; b += 1024) order[atomicAdd(&next[min(counts[b], ORDER_BINS - 1)], 1)] = b;
+}
+
 // Exclusive scan of counts[0..B) -> cu[0..B], n_tokens = cu[B]; one workgroup.
 // With `order`, also the sequences by decreasing length (a counting sort over
 // the lengths, clamped to ORDER_BINS - 1; ties in any order): the attention
 // grid walks them longest first, so that the long sequences' workgroups start
 // first and the short ones fill in around them.
-constexpr int ORDER_BINS = 1024;
 __global__ __launch_bounds__(1024) void pack_scan_kernel(const int* __restrict__ counts, int B,
                                                          int* __restrict__ cu,
                                                          int* __restrict__ n_tokens,
                                                          int* __restrict__ order) {
-    __shared__ int buf[1024];
+    __shared__ int wsum[16];
     __shared__ int next[ORDER_BINS];
     const int tid = threadIdx.x;
     const int per = (B + 1023) / 1024;
     const int lo = min(B, tid * per), hi = min(B, lo + per);
     int local = 0;
     for (int i = lo; i < hi; ++i) local += counts[i];
-    buf[tid] = local;
-    __syncthreads();
-    for (int off = 1; off < 1024; off <<= 1) {  // Hillis-Steele inclusive scan
-        const int v = tid >= off ? buf[tid - off] : 0;
-        __syncthreads();
-        buf[tid] += v;
-        __syncthreads();
-    }
-    int run = buf[tid] - local;  // exclusive prefix of this thread's segment
+    int total;
+    int run = block_excl_scan_1024(local, wsum, total);   // exclusive prefix of this thread's segment
     for (int i = lo; i < hi; ++i) {
         cu[i] = run;
         run += counts[i];
     }
     if (tid == 1023) {
-        cu[B] = buf[1023];
-        *n_tokens = buf[1023];
+        cu[B] = total;
+        *n_tokens = total;
     }
     if (!order) return;   // uniform over the workgroup
-    static_assert(ORDER_BINS == 1024, "one bin per thread");
-    next[tid] = 0;
-    __syncthreads();
-    for (int b = tid; b < B; b += 1024) atomicAdd(&next[min(counts[b], ORDER_BINS - 1)], 1);
-    __syncthreads();
-    // Thread t takes bin 1023 - t, so the inclusive scan runs from the
-    // longest length down; its exclusive value is the bin's first slot.
-    const int n_bin = next[ORDER_BINS - 1 - tid];
-    buf[tid] = n_bin;
-    __syncthreads();
-    for (int off = 1; off < 1024; off <<= 1) {
-        const int v = tid >= off ? buf[tid - off] : 0;
-        __syncthreads();
-        buf[tid] += v;
-        __syncthreads();
-    }
-    next[ORDER_BINS - 1 - tid] = buf[tid] - n_bin;
-    __syncthreads();
-    for (int b = tid; b < B; b += 1024) order[atomicAdd(&next[min(counts[b], ORDER_BINS - 1)], 1)] = b;
+    order_by_length(counts, B, next, wsum, order);
 }
 
 __global__ __launch_bounds__(256) void pack_scatter_kernel(const int* __restrict__ ids,
@@ -120,25 +141,29 @@ __global__ __launch_bounds__(256) void pack_scatter_kernel(const int* __restrict
 
 // The whole packing in one 1024-thread workgroup, for batches of at most
 // PACK1_MAX_POS positions and PACK1_MAX_B sequences (c2, c4: three launches
-// made one).  Positions go in rounds of 1024 in order: each round's mask
-// flags are ranked by a ballot per wave and the waves' counts added in wave
-// order, so every kept token lands where the three-kernel path puts it.  The
-// thread holding position b * S records cu[b], the tokens before it.  The
-// order of the sequences by decreasing length is the same counting sort as
-// in pack_scan_kernel, over counts held in LDS.
-constexpr int PACK1_MAX_POS = 16384, PACK1_MAX_B = 1024;
+// made one).  Positions go in rounds of 1024 in order.  Every round's mask
+// and ids are loaded first; a ballot per wave and round counts the kept
+// tokens, one workgroup scan turns the (round, wave) counts into offsets,
+// and each lane adds the kept tokens below it in its wave's ballot, so every
+// kept token lands where the three-kernel path puts it.  The thread holding
+// position b * S records cu[b], the tokens before it.  The order of the
+// sequences by decreasing length is the same counting sort as in
+// pack_scan_kernel, over counts held in LDS.  Four barriers before the
+// order, three in it.
+constexpr int PACK1_MAX_POS = 8192, PACK1_MAX_B = 1024;
 __global__ __launch_bounds__(1024) void pack_one_kernel(const int* __restrict__ ids, const int* __restrict__ mask,
                                                         int B, int S, int* __restrict__ counts,
                                                         int* __restrict__ cu, int* __restrict__ n_tokens,
                                                         int* __restrict__ tok_id, int* __restrict__ tok_pos,
                                                         int* __restrict__ order) {
-    __shared__ int wcount[16];
+    constexpr int R = PACK1_MAX_POS / 1024;   // rounds of 1024 positions
+    __shared__ int wsum[16];
+    __shared__ int off_s[16 * R];              // per (round, wave): its count, then the tokens before it
     __shared__ int cu_s[PACK1_MAX_B + 1];
+    __shared__ int cnt_s[PACK1_MAX_B];
     __shared__ int next[ORDER_BINS];
-    __shared__ int buf[1024];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int P = B * S;
-    constexpr int R = PACK1_MAX_POS / 1024;
+    const int P = B * S, nr = (P + 1023) / 1024;
     int mv[R], iv[R];   // every round's mask and id, loaded before the first ranking
 #pragma unroll
     for (int r = 0; r < R; ++r) {
@@ -146,61 +171,53 @@ __global__ __launch_bounds__(1024) void pack_one_kernel(const int* __restrict__ 
         mv[r] = p < P ? mask[p] : 0;
         iv[r] = p < P ? ids[p] : 0;
     }
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+        if (r < nr) {   // uniform
+            const int c = __popcll(__ballot(mv[r] != 0));
+            if (lane == 0) off_s[r * 16 + wave] = c;
+            __builtin_amdgcn_sched_barrier(0);   // one round's mask live at a time
+        }
     for (int b = tid; b <= B; b += 1024) cu_s[b] = 0;   // S == 0: every sequence empty
     __syncthreads();
-    int base = 0;
+    // The (round, wave) counts in round-major order, scanned: thread i takes entry i.
+    int total;
+    const int pre = block_excl_scan_1024(tid < 16 * nr ? off_s[tid] : 0, wsum, total);
+    if (tid < 16 * nr) off_s[tid] = pre;   // each thread rewrites only its own entry
+    __syncthreads();
+    // The ballots are taken again below (one instruction each) rather than
+    // the counting pass's sixteen 64-bit masks being held across the scan.
 #pragma unroll
-    for (int r = 0; r < R; ++r) {
-        if (r * 1024 >= P) break;   // uniform
-        const int p = r * 1024 + tid;
-        const bool on = mv[r] != 0;
-        const int id = iv[r];
-        const unsigned long long bal = __ballot(on);
-        if (lane == 0) wcount[wave] = __popcll(bal);
-        __syncthreads();
-        // Lane w < 16 holds wave w's count: the waves before this one, and all.
-        const int c = lane < 16 ? wcount[lane] : 0;
-        int before = lane < wave ? c : 0, total = c;
+    for (int r = 0; r < R; ++r) asm volatile("" : "+v"(mv[r]));
 #pragma unroll
-        for (int o = 32; o > 0; o >>= 1) {   // whole-wave sums: every lane needs them
-            before += __shfl_xor(before, o);
-            total += __shfl_xor(total, o);
+    for (int r = 0; r < R; ++r)
+        if (r < nr) {
+            const int p = r * 1024 + tid;
+            const bool on = mv[r] != 0;
+            const unsigned long long bal = __ballot(on);
+            const unsigned long long below = lane ? (bal & ((~0ull) >> (64 - lane))) : 0ull;
+            const int dst = off_s[r * 16 + wave] + __popcll(below);
+            if (p < P && p % S == 0) cu_s[p / S] = dst;
+            if (on) {
+                tok_id[dst] = iv[r];
+                tok_pos[dst] = p % S;
+            }
+            __builtin_amdgcn_sched_barrier(0);
         }
-        const unsigned long long below = lane ? (bal & ((~0ull) >> (64 - lane))) : 0ull;
-        const int dst = base + before + __popcll(below);
-        if (p < P && p % S == 0) cu_s[p / S] = dst;
-        if (on) {
-            tok_id[dst] = id;
-            tok_pos[dst] = p % S;
-        }
-        base += total;
-        __syncthreads();   // wcount is rewritten next round
-    }
     if (tid == 0) {
-        cu_s[B] = base;
-        *n_tokens = base;
+        cu_s[B] = total;
+        *n_tokens = total;
     }
     __syncthreads();
     for (int b = tid; b <= B; b += 1024) cu[b] = cu_s[b];
-    for (int b = tid; b < B; b += 1024) counts[b] = cu_s[b + 1] - cu_s[b];
-    if (!order) return;   // uniform over the workgroup
-    next[tid] = 0;
-    __syncthreads();
-    for (int b = tid; b < B; b += 1024) atomicAdd(&next[min(cu_s[b + 1] - cu_s[b], ORDER_BINS - 1)], 1);
-    __syncthreads();
-    const int n_bin = next[ORDER_BINS - 1 - tid];
-    buf[tid] = n_bin;
-    __syncthreads();
-    for (int off = 1; off < 1024; off <<= 1) {
-        const int v = tid >= off ? buf[tid - off] : 0;
-        __syncthreads();
-        buf[tid] += v;
-        __syncthreads();
+    for (int b = tid; b < B; b += 1024) {
+        const int n = cu_s[b + 1] - cu_s[b];
+        cnt_s[b] = n;
+        counts[b] = n;
     }
-    next[ORDER_BINS - 1 - tid] = buf[tid] - n_bin;
+    if (!order) return;   // uniform over the workgroup
     __syncthreads();
-    for (int b = tid; b < B; b += 1024)
-        order[atomicAdd(&next[min(cu_s[b + 1] - cu_s[b], ORDER_BINS - 1)], 1)] = b;
+    order_by_length(cnt_s, B, next, wsum, order);
 }
 
 hipError_t launch_pack(const int* ids, const int* mask, int B, int S, int* counts, int* cu,
