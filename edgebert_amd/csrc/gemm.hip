@@ -1743,8 +1743,9 @@ hipError_t launch_gemm_f32(const GemmArgs& a, int epi, hipStream_t s) {
     //  * otherwise 128 x 128 tiles, 64-deep k-tiles, 8 waves (two per SIMD).
     //  * split-K (a.splits > 1, bias-free products only): each split is a work
     //    item of its own, written to its own partial output; mid-size split
-    //    products run 128 x 96 x 32 tiles where N is whole 96-column panels,
-    //    else 128 x 128 x 32, two workgroups per CU (mid_splits).
+    //    products run 128 x 96 x 32 tiles where N is whole 96-column panels
+    //    and there are fewer 128 x 128 tiles than CUs, else 128 x 128 x 32,
+    //    two workgroups per CU (mid_splits picks the split count to match).
     const int S = a.splits > 1 ? a.splits : 1;
     //  * at most 64 rows: the few-token kernel (gemm_skinny_kernel); bias-free
     //    products split over K as below.
