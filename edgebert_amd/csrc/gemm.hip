@@ -1740,6 +1740,12 @@ hipError_t launch_gemm_f32(const GemmArgs& a, int epi, hipStream_t s) {
     //  * wide outputs over a short K with many tiles per CU: 32-deep k-tiles,
     //    two workgroups per CU, so one workgroup's GELU epilogue runs beside
     //    the other's MFMAs;
+    //  * where 128 x 128 tiles would need more than one round by the padded
+    //    row count but 128 x 96 tiles come to at most 1.5 per CU (N whole
+    //    96-column panels): those, two workgroups per CU.  The busiest CU then
+    //    has 0.75 of a 128 x 128 tile's work if the real rows fill one round,
+    //    1.5 of it if they fill more, against 1 or 2 (QKV at 4,096 padded
+    //    rows: 53.0 -> 41.8 us dense, 31.2 -> 28.7 us for c2's 2,424 rows);
     //  * otherwise 128 x 128 tiles, 64-deep k-tiles, 8 waves (two per SIMD).
     //  * split-K (a.splits > 1, bias-free products only): each split is a work
     //    item of its own, written to its own partial output; mid-size split
@@ -1769,6 +1775,9 @@ hipError_t launch_gemm_f32(const GemmArgs& a, int epi, hipStream_t s) {
     if (wide192) return launch_persistent<256, 192, 32, 4, 2, 2>(a, epi, s, 1);
     if (ok && a.K % 32 == 0 && a.N >= 1536 && a.K < 1024 && tiles128 >= 8 * (int64_t)cu_count() && S == 1)
         return launch_persistent<128, 128, 32, 2, 2, 2>(a, epi, s, 2);
+    if (ok && S == 1 && a.N % 96 == 0 && a.K % 32 == 0 && tiles128 > (int64_t)cu_count() &&
+        2 * (int64_t)((a.M_max + 127) / 128) * (a.N / 96) <= 3 * (int64_t)cu_count())
+        return launch_persistent<128, 96, 32, 4, 1, 2>(a, epi, s, 2);
     if (ok && a.K % (64 * S) == 0)
         return launch_persistent<128, 128, 64, 2, 4, 2>(a, epi, s, 1);
     if (ok && a.K % (32 * S) == 0)

@@ -116,6 +116,8 @@ def test_gemm_f32_row_stride_past_32bit_offsets(env):
     (12000, 1152, 384, 0),     # 128 x 96 tiles in place of 1.1 rounds of 256 x 192 (bias)
     (20000, 1536, 384, 3),     # 128 x 96 tiles in place of 1.8 rounds of 256 x 256 (no bias)
     (40000, 576, 256, 1),      # 128 x 96 tiles, 8 k-tiles, ragged last row block (GELU)
+    (4000, 1152, 384, 0),      # 128 x 96 tiles in place of 1.1 rounds of 128 x 128 (bias), ragged rows
+    (3000, 1536, 384, 1),      # the same with GELU
     (40000, 512, 160, 3),      # 256 x 256 tiles, no bias, 5 k-tiles
     (9000, 1024, 384, 1),      # 128 x 128 tiles beside the 128 x 384 case (N not whole panels)
     (500, 256, 96, 0),         # K % 64 != 0: 32-deep k-tiles
@@ -145,7 +147,8 @@ def test_gemm_f32_dispatch_paths(env, M, N, K, epi):
 @pytest.mark.parametrize("M,N,K,epi", [
     (4100, 1152, 384, 0), (8192, 384, 1536, 3), (33000, 1536, 384, 1), (32768, 1152, 384, 0),
     (33000, 1152, 384, 1), (90000, 576, 256, 3), (40000, 512, 160, 3), (9000, 1024, 384, 1),
-    (500, 256, 96, 0), (2000, 384, 1536, 3), (8100, 1536, 384, 1), (12000, 1152, 384, 0)])
+    (500, 256, 96, 0), (2000, 384, 1536, 3), (8100, 1536, 384, 1), (12000, 1152, 384, 0),
+    (4000, 1152, 384, 0)])
 def test_gemm_f32_split_products(env, M, N, K, epi):
     """EBH_DTYPE_F32_BF16X6: fp32 products formed from six bf16 MFMA products
     of three-way bf16 splits, on every tile configuration of the fp32
