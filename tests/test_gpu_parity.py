@@ -270,6 +270,29 @@ def test_bf16_minilm_few_tokens(eb, oracle_mod, weights_for, B, S, lo, hi):
     assert cos >= BF16_MIN_COS
 
 
+@pytest.mark.parametrize("B,lo", [(64, 128), (96, 128), (128, 8)])
+def test_mid_size_batches_match_oracle(eb, oracle_mod, weights_for, B, lo):
+    """MiniLM batches of 8k-16k padded positions, dense or ragged, through the
+    host-buffer entry point (too few 128-row blocks for the fused GEMM +
+    LayerNorm, so the kernels are the device path's): FFN up (and at 96 x 128
+    the QKV projection) on 128 x
+    96 tiles in place of the wide ones; the attention-output and FFN-down
+    products split on 128 x 96 tiles (64 x 128), or on 128 x 128 tiles (96 x
+    128, 128 x 128); fewer sequences than CUs, so the pool sums 32-row chunks;
+    packing in one workgroup (64 x 128) or in three kernels.  16 sequences
+    against the oracle's unpadded run; every row unit-norm."""
+    from edgebert_amd.synth import InputSpec, MINILM_L6, make_inputs
+    spec = InputSpec(f"mid{B}", MINILM_L6, B, 128, lo, 128, 90 + B)
+    w = weights_for(MINILM_L6)
+    ids, mask, _ = make_inputs(spec)
+    got = gpu_model(eb, MINILM_L6, w).encode_ids(ids, mask, normalize=True)
+    np.testing.assert_allclose(np.linalg.norm(got.astype(np.float64), axis=1), 1.0, atol=1e-5)
+    sel = np.arange(1, B, B // 16)[:16]
+    want = oracle_mod.OracleModel(MINILM_L6, w).encode_unpadded(ids[sel], mask[sel], normalize=True)
+    err, cos = _report(f"MiniLM {B}x128 (lengths {lo}-128)", got[sel], want)
+    assert err <= FP32_MAX_ABS and cos >= FP32_MIN_COS
+
+
 def test_ragged_large_batch_host_path(eb, oracle_mod, weights_for):
     """256 sentences of 8..128 tokens padded to 128 through the host-buffer
     entry point: the host counts the packed rows (about half of B*S), too few
