@@ -1050,6 +1050,9 @@ __global__ __launch_bounds__(POOL_NT) void pool_finish_kernel(const float* __res
     }
     pool_finish_row(v, t, F, len, S, normalize, out + (int64_t)b * H, wsum);
 }
+
+// One workgroup of POOL_WAVES waves per sequence (batches of at least as many
+// sequences as CUs, one chunk, or other widths).
 constexpr int POOL_WAVES = 8;
 
 template <int NC>
